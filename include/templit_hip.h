@@ -1,0 +1,355 @@
+/*
+ * templit_hip.h -- C-ABI of libtemplit_hip.so, the gfx950 (MI355X) kernel
+ * library behind hip::Runtime.
+ *
+ * This is the drop-in boundary for the TempLit runtime backend. The Metal
+ * backend reaches its GPU through metal-cpp and 31 kernels that
+ * src/my_metal/runtime.cpp loads by name (runtime.cpp:251-282) from
+ * include/my_metal/math.metal. Here every kernel name becomes one extern "C"
+ * entry point taking plain device pointers, sizes and a stream:
+ *
+ *   - every function returns an int: a hipError_t code, 0 on success;
+ *   - pointers are device pointers unless named host_*; they are borrowed
+ *     only for the work enqueued by the call;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream);
+ *   - work is enqueued asynchronously in call order on `stream` (the Metal
+ *     runtime's single serial compute encoder, runtime.cpp:290-317);
+ *   - shapes are uint32 (the reference's rtensor::index_type,
+ *     include/RTensor/RTensor.h:18-21); element counts are size_t;
+ *   - no C++ types or exceptions cross this boundary. Shape validation that
+ *     the reference performs in C++ (std::invalid_argument etc.) is done by
+ *     the host runtime above this layer; these functions only reject
+ *     arguments they cannot execute (hipErrorInvalidValue).
+ *
+ * Each declaration cites the reference interface it replaces (path:line in
+ * the TempLit tree).
+ */
+#ifndef TEMPLIT_HIP_H
+#define TEMPLIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Device, memory, streams, events, graphs
+ * ------------------------------------------------------------------------- */
+
+/* metal::init (src/my_metal/metal.cpp:18-27): select the device once;
+ * idempotent for the same device. */
+int tlh_init(int device);
+int tlh_device_count(int *count);
+const char *tlh_error_string(int code);
+int tlh_device_synchronize(void);
+
+/* Command queue / command buffer (runtime.cpp:238, 290-317). */
+int tlh_stream_create(void **stream);
+int tlh_stream_destroy(void *stream);
+/* cmdBuff_->waitUntilCompleted (runtime.cpp:310-317). */
+int tlh_stream_synchronize(void *stream);
+
+/* device->newBuffer (include/my_metal/storage.h:13-16) and its release. */
+int tlh_malloc(void **ptr, size_t bytes);
+int tlh_free(void *ptr);
+/* Pinned host staging memory for stream-ordered host<->device copies. */
+int tlh_host_alloc(void **host_ptr, size_t bytes);
+int tlh_host_free(void *host_ptr);
+
+/* Storage::write / read (include/my_metal/storage.h:26-40); asynchronous on
+ * `stream`: synchronise before reusing or reading the host buffer. */
+int tlh_memcpy_h2d(void *dst, const void *host_src, size_t bytes, void *stream);
+int tlh_memcpy_d2h(void *host_dst, const void *src, size_t bytes, void *stream);
+/* Storage::clone (storage.h:45-50) and the blit copy of scatter_add_rows
+ * (runtime.cpp:989-1009). */
+int tlh_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+/* Storage::fill (storage.h:41-43) and the blit zero-fill of scatter_index
+ * (runtime.cpp:1018-1027). Kernel fills, safe inside captured graphs. */
+int tlh_fill_f32(float *dst, float value, size_t n, void *stream);
+int tlh_fill_u32(uint32_t *dst, uint32_t value, size_t n, void *stream);
+/* Storage::compare (storage.h:52-59): byte equality. `scratch` is one device
+ * int. Synchronous. */
+int tlh_compare(const void *a, const void *b, size_t bytes, int *host_equal,
+                int *scratch, void *stream);
+
+int tlh_event_create(void **event);
+int tlh_event_record(void *event, void *stream);
+int tlh_event_synchronize(void *event);
+int tlh_event_elapsed_ms(void *start, void *end, float *host_ms);
+int tlh_event_destroy(void *event);
+
+/* Command-buffer record/commit as a hipGraph (runtime.cpp:290-309). */
+int tlh_graph_begin_capture(void *stream);
+int tlh_graph_end_capture(void *stream, void **exec);
+int tlh_graph_launch(void *exec, void *stream);
+int tlh_graph_destroy(void *exec);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise (math.metal:401-548, 821-855, 1045-1050)
+ * ------------------------------------------------------------------------- */
+
+/* Broadcast binary ops, kernels add/sub/hadamard/divide
+ * (math.metal:401-510) launched by call_binary_op (runtime.cpp:65-95).
+ * `out` is contiguous with `ndim` dims `out_shape`; stride_a / stride_b are
+ * the element strides of a and b aligned to out, 0 on broadcast dims -- what
+ * broadcast_strides (runtime.cpp:18-39) computes. ndim <= 8. `out` may alias
+ * a or b when it has their shape (in-place, execute.h:249). */
+int tlh_add(const float *a, const float *b, float *out, uint32_t ndim,
+            const uint32_t *out_shape, const uint32_t *stride_a,
+            const uint32_t *stride_b, void *stream);
+int tlh_sub(const float *a, const float *b, float *out, uint32_t ndim,
+            const uint32_t *out_shape, const uint32_t *stride_a,
+            const uint32_t *stride_b, void *stream);
+int tlh_hadamard(const float *a, const float *b, float *out, uint32_t ndim,
+                 const uint32_t *out_shape, const uint32_t *stride_a,
+                 const uint32_t *stride_b, void *stream);
+int tlh_divide(const float *a, const float *b, float *out, uint32_t ndim,
+               const uint32_t *out_shape, const uint32_t *stride_a,
+               const uint32_t *stride_b, void *stream);
+
+/* Scalar ops add_scalar / divide_scalar / pow_scalar (math.metal:427-434,
+ * 511-518, 527-534; call_scalar_op runtime.cpp:116-136). */
+int tlh_add_scalar(const float *a, float scalar, float *out, size_t n, void *stream);
+int tlh_divide_scalar(const float *a, float scalar, float *out, size_t n, void *stream);
+int tlh_pow_scalar(const float *a, float exponent, float *out, size_t n, void *stream);
+
+/* Unary ops sqrt / exp / sigmoid (math.metal:519-548; call_unary_op
+ * runtime.cpp:97-114), GELU / GELU_derivative (math.metal:821-855,
+ * runtime.cpp:1073-1081), copy (math.metal:1045-1050, runtime.cpp:1170-1186). */
+int tlh_sqrt(const float *a, float *out, size_t n, void *stream);
+int tlh_exp(const float *a, float *out, size_t n, void *stream);
+int tlh_sigmoid(const float *a, float *out, size_t n, void *stream);
+int tlh_gelu(const float *a, float *out, size_t n, void *stream);
+int tlh_gelu_derivative(const float *a, float *out, size_t n, void *stream);
+int tlh_copy(const float *a, float *out, size_t n, void *stream);
+
+/* Fused GELU backward: out = grad * GELU'(x). Replaces the executor's
+ * GELU_derivative + hadamard pair (autograd of expr/gelu.h). */
+int tlh_gelu_backward(const float *grad, const float *x, float *out, size_t n,
+                      void *stream);
+
+/* transpose (math.metal:566-584, runtime.cpp:529-569): `out` is contiguous
+ * with `ndim` dims `out_shape`; in_strides are the input's strides with the
+ * two swapped axes exchanged (runtime.cpp:549-553). Any permutation of
+ * strides works. ndim <= 8. */
+int tlh_transpose(const float *a, float *out, uint32_t ndim,
+                  const uint32_t *out_shape, const uint32_t *in_strides,
+                  void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Matrix products (math.metal:13-400, runtime.cpp:375-505)
+ * ------------------------------------------------------------------------- */
+
+/* Runtime::mult: C[b..,M,N] = A[b..,M,K] . B[b..,K,N] in fp32 on the MFMA
+ * units. Row/column element strides of each operand (a_rs, a_cs, ...) follow
+ * runtime.cpp:458-463; one of each pair must be 1 (column-major operands run
+ * the transposed-operand kernels). C must be row-major (c_cs == 1). Batch
+ * dims (<= 4) decode like matmul_contiguous (math.metal:48-61): batch element
+ * strides per operand, 0 = broadcast (runtime.cpp:437-446). */
+int tlh_matmul(const float *a, const float *b, float *c, uint32_t M, uint32_t K,
+               uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs,
+               uint32_t b_cs, uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+               const uint32_t *batch_shape, const uint32_t *batch_stride_a,
+               const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
+               void *stream);
+
+/* Fused GEMM used by the program layer (no reference counterpart; it fuses
+ * EXPR_LINEAR = mult + in-place bias add (execute.h:241-252), the GELU that
+ * follows, the residual add, and MULT_LHS/RHS_DERIVATIVE's transposes
+ * (execute.h:187-232) into one launch). */
+enum {
+  TLH_EPI_STORE = 0,    /* C = acc (+bias) (+beta*C) (+residual) */
+  TLH_EPI_GELU = 1,     /* aux = acc + bias; C = GELU(aux) */
+  TLH_EPI_GELU_BWD = 2  /* C = acc * GELU'(aux) */
+};
+
+typedef struct tlh_gemm_desc {
+  const float *a;        /* op(A) [M,K]: stored [M,K] (lda), or [K,M] if trans_a */
+  const float *b;        /* op(B) [K,N]: stored [K,N] (ldb), or [N,K] if trans_b */
+  float *c;              /* [M,N] row stride ldc, or head layout (remap_*) */
+  const float *bias;     /* [N] or NULL */
+  const float *residual; /* indexed like c, or NULL */
+  float *aux;            /* GELU pre-activation, indexed like c, or NULL */
+  float *workspace;      /* split-K partials, tlh_gemm_workspace_size elems */
+  int32_t m, n, k;
+  int32_t lda, ldb, ldc;
+  int32_t trans_a, trans_b;
+  float beta;
+  int32_t epilogue;
+  /* if remap_h > 0: element (m = b*remap_t + t, n = h*remap_d + d) is stored
+   * at ((b*remap_h + h)*remap_t + t)*remap_d + d */
+  int32_t remap_t, remap_h, remap_d;
+} tlh_gemm_desc;
+
+int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
+/* fp32 elements of workspace tlh_gemm wants for `desc` (0: none needed). */
+int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
+
+/* ---------------------------------------------------------------------------
+ * Reductions (math.metal:549-564, 618-777, 955-983)
+ * ------------------------------------------------------------------------- */
+
+/* sum of all elements (math.metal:549-564, runtime.cpp:506-518). */
+int tlh_sum(const float *a, size_t n, float *out, void *stream);
+/* sum_to_shape (math.metal:618-679, runtime.cpp:661-739): `a` is contiguous
+ * with `ndim` dims a_shape; `out` is contiguous with the rank-aligned shape
+ * out_shape (1 on reduced dims, equal otherwise). ndim <= 8. */
+int tlh_sum_to_shape(const float *a, float *out, uint32_t ndim,
+                     const uint32_t *a_shape, const uint32_t *out_shape,
+                     void *stream);
+/* max_to_shape (math.metal:681-714, runtime.cpp:595-659,741-745); same
+ * shape rules as tlh_sum_to_shape. */
+int tlh_max_to_shape(const float *a, float *out, uint32_t ndim,
+                     const uint32_t *a_shape, const uint32_t *out_shape,
+                     void *stream);
+/* argmax (math.metal:715-777, runtime.cpp:850-918): index of the first
+ * maximum (lowest index on ties; NaNs never win). n >= 1. */
+int tlh_argmax(const float *a, size_t n, uint32_t *out_index, void *stream);
+/* Row argmax: out[r] = argmax over a[r, 0:cols] (greedy decoding). */
+int tlh_argmax_rows(const float *a, size_t rows, uint32_t cols,
+                    uint32_t *out_index, void *stream);
+/* accumulate_gradient_squared_norm (math.metal:955-983,
+ * runtime.cpp:1083-1101): *squared_norm += sum(g^2). */
+int tlh_accumulate_gradient_squared_norm(const float *g, size_t n,
+                                         float *squared_norm, void *stream);
+/* Multi-tensor version: one launch over `count` tensors (device arrays of
+ * pointers and sizes); *squared_norm += sum over all. */
+int tlh_gradient_squared_norm_multi(const float *const *grads,
+                                    const uint64_t *sizes, uint32_t count,
+                                    float *squared_norm, void *stream);
+/* Column sums: out[c] (+)= sum_r a[r, c]  (bias gradients, the
+ * sum_to_shape [.., N] -> [1, N] case). beta scales the old out. */
+int tlh_column_sum(const float *a, size_t rows, uint32_t cols, float *out,
+                   float beta, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Row ops (math.metal:857-953, runtime.cpp:747-841, 1031-1072)
+ * ------------------------------------------------------------------------- */
+
+/* softmax over the last dim (math.metal:857-882, runtime.cpp:747-766). */
+int tlh_softmax(const float *x, float *out, size_t rows, uint32_t cols,
+                void *stream);
+/* Softmax backward: out = y * (g - sum(g*y)) per row (EXPR_SFTMX_DERIVATIVE,
+ * execute.h:291-308). out may alias g. */
+int tlh_softmax_backward(const float *g, const float *y, float *out,
+                         size_t rows, uint32_t cols, void *stream);
+/* cross_entropy_rows (math.metal:884-910, runtime.cpp:768-804): loss[r] =
+ * max + log(sum exp(x - max)) - x[t]; target >= vocab -> +INF. */
+int tlh_cross_entropy_rows(const float *logits, const uint32_t *targets,
+                           float *losses, size_t rows, uint32_t vocab,
+                           void *stream);
+/* cross_entropy_rows_backward (math.metal:912-953, runtime.cpp:806-841):
+ * grad = softmax(x) - onehot(t); target >= vocab -> row of +INF. If
+ * row_scale != NULL each row is multiplied by row_scale[r] (fuses the
+ * upstream hadamard of autograd). */
+int tlh_cross_entropy_rows_backward(const float *logits, const uint32_t *targets,
+                                    float *grad, size_t rows, uint32_t vocab,
+                                    const float *row_scale, void *stream);
+/* RMS (runtime.cpp:1031-1052): rms[r] = sqrt(sum(x^2)/cols + eps). */
+int tlh_rms(const float *x, float *rms, size_t rows, uint32_t cols, float eps,
+            void *stream);
+/* RMSNorm (runtime.cpp:1060-1072): y = x / rms (* gain[c] if gain != NULL);
+ * rms_out (nullable) receives rms per row. Single pass. */
+int tlh_rms_norm(const float *x, const float *gain, float *y, float *rms_out,
+                 size_t rows, uint32_t cols, float eps, void *stream);
+/* RMSNorm backward (EXPR_RMSN_DERIVATIVE, execute.h:330-356, extended with
+ * the optional gain): with n = x/rms, gy = g*gain,
+ * dx = (gy - n*mean(gy*n)) / rms; dx_out = beta*dx_out + dx. grad_gain
+ * (nullable) receives sum over rows of g*n (overwritten). */
+int tlh_rms_norm_backward(const float *g, const float *x, const float *gain,
+                          float *dx, float *grad_gain, size_t rows,
+                          uint32_t cols, float eps, float beta, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Embedding (math.metal:778-820, runtime.cpp:920-1030)
+ * ------------------------------------------------------------------------- */
+
+/* embedding_lookup / gather_rows (math.metal:778-793, runtime.cpp:920-950):
+ * out[i, :] = weights[ids[i], :]. Bit-exact copy; ids >= rows -> hipErrorInvalidValue
+ * is not detected on device: callers validate (reference does not check). */
+int tlh_embedding_lookup(const float *weights, uint32_t rows, uint32_t dim,
+                         const uint32_t *ids, size_t n_ids, float *out,
+                         void *stream);
+/* Fused token+position embedding: out[b,t,:] = tok[ids[b,t],:] + pos[t,:]
+ * (GPT.h:62-64: add(embedding(input), embedding(positions))). */
+int tlh_embedding_add_positions(const float *tok, const float *pos,
+                                const uint32_t *ids, uint32_t batch,
+                                uint32_t seq, uint32_t dim, float *out,
+                                void *stream);
+/* scatter_add_rows (math.metal:794-820, runtime.cpp:952-981): dst[ids[i],:]
+ * += values[i,:] with float atomics (order nondeterministic). The caller
+ * pre-fills dst (base copy or zero, runtime.cpp:983-1030). */
+int tlh_scatter_add_rows(const float *values, const uint32_t *ids, size_t n_ids,
+                         uint32_t dim, float *dst, void *stream);
+/* Deterministic embedding backward: dst[r,:] = beta*dst[r,:] + sum over i
+ * with ids[i]==r of values[i,:] in increasing i. `order` / `offsets` come
+ * from tlh_sort_ids (scratch of n_ids + rows + 1 uint32). */
+int tlh_scatter_rows_sorted(const float *values, const uint32_t *order,
+                            const uint32_t *offsets, uint32_t rows,
+                            uint32_t dim, float *dst, float beta, void *stream);
+/* Stable counting sort of ids into order[n_ids] and offsets[rows+1]
+ * (device scratch `counts` of rows+1 uint32). */
+int tlh_sort_ids(const uint32_t *ids, size_t n_ids, uint32_t rows,
+                 uint32_t *order, uint32_t *offsets, uint32_t *counts,
+                 void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Attention (no reference op: replaces the decomposed chain of
+ * include/nn/multi_head.h:33-55)
+ * ------------------------------------------------------------------------- */
+
+/* Fused causal multi-head attention forward:
+ *   O = softmax(Q K^T * scale + mask) V,  mask = 0 / -inf above the diagonal
+ * q, k, v: [B, H, T, D] contiguous; o: [B, T, H*D] (heads merged, the
+ * layout merge_last_dims produces) when o_merged != 0, else [B, H, T, D];
+ * lse: [B, H, T] log-sum-exp of the scaled masked scores (for backward).
+ * D must be 64. */
+int tlh_attention_forward(const float *q, const float *k, const float *v,
+                          float *o, float *lse, uint32_t batch, uint32_t heads,
+                          uint32_t seq, uint32_t head_dim, float scale,
+                          int causal, int o_merged, void *stream);
+/* Backward. do_ and o in the same layout as the forward's o (o_merged);
+ * dq, dk, dv: [B, H, T, D] unless dqkv_merged != 0, then [B, T, H*D].
+ * `delta` is scratch [B, H, T]. */
+int tlh_attention_backward(const float *q, const float *k, const float *v,
+                           const float *o, const float *do_, const float *lse,
+                           float *delta, float *dq, float *dk, float *dv,
+                           uint32_t batch, uint32_t heads, uint32_t seq,
+                           uint32_t head_dim, float scale, int causal,
+                           int o_merged, int dqkv_merged, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Optimiser (math.metal:985-1043, runtime.cpp:1103-1168)
+ * ------------------------------------------------------------------------- */
+
+/* clip_gradient (math.metal:985-1006): out = g * min(1, max_norm /
+ * sqrt(max(*squared_norm, 1e-12))). out may alias g. */
+int tlh_clip_gradient(const float *g, const float *squared_norm, float max_norm,
+                      float *out, size_t n, void *stream);
+/* adamW (math.metal:1008-1043, runtime.cpp:1129-1168): beta1, beta2, decay,
+ * lr are 1-element device tensors (include/optimiser/AdamW.h:15-39). out may
+ * alias param. step >= 1. */
+int tlh_adamw(const float *param, const float *grad, float *out, float *m1,
+              float *m2, const float *beta1, const float *beta2,
+              const float *decay, const float *lr, float eps, uint32_t step,
+              size_t n, void *stream);
+
+/* Multi-tensor fused clip + AdamW: one launch updates `count` tensors in
+ * place. Device arrays: params/grads/m1/m2 pointers, sizes, steps (uint32
+ * per tensor: the per-parameter step_ of AdamW.h:42,78). If squared_norm
+ * != NULL the gradient is scaled by min(1, max_norm/sqrt(max(s,1e-12)))
+ * first (Compiled::step(max_norm), compile.h:236-258). */
+int tlh_adamw_multi(float *const *params, const float *const *grads,
+                    float *const *m1, float *const *m2, const uint64_t *sizes,
+                    const uint32_t *steps, uint32_t count, const float *beta1,
+                    const float *beta2, const float *decay, const float *lr,
+                    float eps, const float *squared_norm, float max_norm,
+                    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEMPLIT_HIP_H */

@@ -1,0 +1,517 @@
+// fp32 GEMM on the CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
+//
+// Replaces the Metal matmul kernels K1-K3 (include/my_metal/math.metal:13-400,
+// launched from src/my_metal/runtime.cpp:375-505). Differences by design:
+//  * one kernel family covers contiguous, transposed-operand (A^T.B, A.B^T)
+//    and masked edge tiles, so the executor's materialised transposes can be
+//    skipped by callers that know the layout;
+//  * fused epilogues (bias, residual, GELU, GELU', head-layout store);
+//  * split-K with a deterministic reduction for the tall-K weight gradients.
+//
+// Tile: BM x BN per 256-thread block (4 waves in a 2x2 grid), BK = 16,
+// LDS double-buffered with a register prefetch of the next K tile.
+// MFMA operand mapping (32x32x2, 64 lanes): lane l supplies A[m=l%32][k=l/32]
+// and B[k=l/32][n=l%32]; accumulator v of lane l holds
+// D[8*(v/4) + 4*(l/32) + v%4][l%32]. Within a K tile the two MFMA k-slots
+// are assigned actual k = slot*(BK/2) + s, so a lane reads BK/2 consecutive
+// k of one row of a K-contiguous LDS tile with ds_read_b128.
+#include "common.h"
+#include "gemm.h"
+
+#include <algorithm>
+
+namespace tlh {
+namespace {
+
+constexpr int kBK = 16;
+constexpr int kPad = 4;
+
+struct GemmParams {
+  const float *A;
+  const float *B;
+  float *C;
+  const float *bias;
+  const float *residual;
+  float *aux;
+  float *workspace;
+  int M, N, K;
+  int lda, ldb, ldc;
+  float beta;
+  int epilogue;
+  int remap_t, remap_h, remap_d;
+  int batch_ndim;
+  uint32_t batch_shape[4];
+  uint32_t bsa[4], bsb[4], bsc[4];
+  int splits;
+  int k_chunk;
+  int tiles_n;
+};
+
+__device__ inline size_t out_index(const GemmParams &p, int m, int n) {
+  if (p.remap_h > 0) {
+    const int b = m / p.remap_t, t = m - b * p.remap_t;
+    const int h = n / p.remap_d, d = n - h * p.remap_d;
+    return ((size_t(b) * p.remap_h + h) * p.remap_t + t) * p.remap_d + d;
+  }
+  return size_t(m) * p.ldc + n;
+}
+
+// Applies the epilogue to one output element. `C` already carries the batch
+// offset; bias/residual/aux are only used for batch == 1 (host-checked).
+__device__ inline void epilogue_store(const GemmParams &p, float *C, int m, int n,
+                                      float v) {
+  const size_t idx = out_index(p, m, n);
+  if (p.bias) v += p.bias[n];
+  if (p.beta != 0.0f) v += p.beta * C[idx];
+  if (p.residual) v += p.residual[idx];
+  if (p.epilogue == kEpiGelu) {
+    p.aux[idx] = v;
+    v = gelu_fwd(v);
+  } else if (p.epilogue == kEpiGeluBwd) {
+    v *= gelu_grad(p.aux[idx]);
+  }
+  C[idx] = v;
+}
+
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+  constexpr int BK = kBK;
+  constexpr int TM = WM / 32;
+  constexpr int TN = WN / 32;
+  constexpr int WAVES_N = BN / WN;
+  static_assert((BM / WM) * (BN / WN) == 4, "4 waves per block");
+  // LDS tile geometry (floats). K-contiguous tiles: [rows][BK+pad];
+  // row-contiguous tiles: [BK][rows+pad].
+  constexpr int A_LD = TA ? (BM + kPad) : (BK + kPad);
+  constexpr int B_LD = TB ? (BK + kPad) : (BN + kPad);
+  constexpr int A_TILE = TA ? BK * A_LD : BM * A_LD;
+  constexpr int B_TILE = TB ? BN * B_LD : BK * B_LD;
+  constexpr int A_CHUNKS = BM * BK / 4 / 256;
+  constexpr int B_CHUNKS = BN * BK / 4 / 256;
+  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
+
+  __shared__ __attribute__((aligned(16))) float smem[2 * (A_TILE + B_TILE)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+  const int r = lane & 31;
+  const int hk = lane >> 5;
+
+  const int tile = blockIdx.x;
+  const int tm = tile / p.tiles_n;
+  const int tn = tile - tm * p.tiles_n;
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+
+  const float *A = p.A;
+  const float *B = p.B;
+  float *C = p.C;
+  int k_begin = 0, k_end = p.K;
+  if (p.splits > 1) {
+    k_begin = blockIdx.z * p.k_chunk;
+    k_end = min(p.K, k_begin + p.k_chunk);
+    C = p.workspace + size_t(blockIdx.z) * p.M * p.N;
+  } else if (p.batch_ndim > 0) {
+    uint32_t rem = blockIdx.z;
+    size_t oa = 0, ob = 0, oc = 0;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+      const uint32_t c = rem % p.batch_shape[d];
+      rem /= p.batch_shape[d];
+      oa += size_t(c) * p.bsa[d];
+      ob += size_t(c) * p.bsb[d];
+      oc += size_t(c) * p.bsc[d];
+    }
+    A += oa;
+    B += ob;
+    C += oc;
+  }
+
+  // ---- global -> register prefetch ----------------------------------------
+  f4 ra[A_CHUNKS], rb[B_CHUNKS];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + i * 256;
+      int row, col; // in stored layout
+      if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+      else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
+      const int grow = TA ? (k0 + row) : (m0 + row);
+      const int gcol = TA ? (m0 + col) : (k0 + col);
+      const int row_lim = TA ? k_end : p.M;
+      const int col_lim = TA ? p.M : k_end;
+      const float *src = A + size_t(grow) * p.lda + gcol;
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (grow < row_lim) {
+        if (VEC && gcol + 3 < col_lim) {
+          v = *reinterpret_cast<const f4 *>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (gcol + j < col_lim) v[j] = src[j];
+        }
+      }
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int c = tid + i * 256;
+      int row, col;
+      if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+      else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
+      const int grow = TB ? (n0 + row) : (k0 + row);
+      const int gcol = TB ? (k0 + col) : (n0 + col);
+      const int row_lim = TB ? p.N : k_end;
+      const int col_lim = TB ? k_end : p.N;
+      const float *src = B + size_t(grow) * p.ldb + gcol;
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (grow < row_lim) {
+        if (VEC && gcol + 3 < col_lim) {
+          v = *reinterpret_cast<const f4 *>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (gcol + j < col_lim) v[j] = src[j];
+        }
+      }
+      rb[i] = v;
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    float *as = smem + buf * (A_TILE + B_TILE);
+    float *bs = as + A_TILE;
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + i * 256;
+      int row, col;
+      if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+      else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
+      *reinterpret_cast<f4 *>(as + row * A_LD + col) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int c = tid + i * 256;
+      int row, col;
+      if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+      else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
+      *reinterpret_cast<f4 *>(bs + row * B_LD + col) = rb[i];
+    }
+  };
+
+  f16x acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int a_row0 = wm * WM + r; // + i*32
+  const int b_col0 = wn * WN + r; // + j*32
+
+  auto compute_tile = [&](int buf) {
+    const float *as = smem + buf * (A_TILE + B_TILE);
+    const float *bs = as + A_TILE;
+#pragma unroll
+    for (int s4 = 0; s4 < BK / 8; ++s4) {
+      const int kb = hk * (BK / 2) + s4 * 4; // first of 4 consecutive k
+      f4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = a_row0 + i * 32;
+        if (!TA) {
+          af[i] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) af[i][q] = as[(kb + q) * A_LD + m];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = b_col0 + j * 32;
+        if (TB) {
+          bf[j] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bf[j][q] = bs[(kb + q) * B_LD + n];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[j][q],
+                                                             acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = (k_end > k_begin) ? (k_end - k_begin + BK - 1) / BK : 0;
+  if (nk > 0) {
+    load_tile(k_begin);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * BK);
+      compute_tile(cur);
+      if (kt + 1 < nk) store_tile(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue --------------------------------------------------------------
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WN + j * 32 + r;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
+        if (m >= p.M) continue;
+        if (p.splits > 1) {
+          C[size_t(m) * p.N + n] = acc[i][j][v];
+        } else {
+          epilogue_store(p, C, m, n, acc[i][j][v]);
+        }
+      }
+    }
+  }
+}
+
+// Sums the split-K partials and applies the epilogue; deterministic order.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
+  const size_t total = size_t(p.M) * p.N;
+  const size_t plane = total;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += size_t(gridDim.x) * blockDim.x) {
+    float s = 0.f;
+    for (int z = 0; z < p.splits; ++z) s += p.workspace[z * plane + i];
+    const int m = int(i / p.N);
+    const int n = int(i - size_t(m) * p.N);
+    epilogue_store(p, p.C, m, n, s);
+  }
+}
+
+struct TileCfg {
+  int bm, bn;
+};
+
+template <int BM, int BN, int WM, int WN>
+void launch_cfg(const GemmParams &p, bool ta, bool tb, bool vec, dim3 grid,
+                hipStream_t s) {
+#define TLH_GEMM_CASE(TA_, TB_, V_)                                              \
+  if (ta == TA_ && tb == TB_ && vec == V_) {                                     \
+    gemm_mfma_kernel<BM, BN, WM, WN, TA_, TB_, V_><<<grid, 256, 0, s>>>(p);       \
+    return;                                                                      \
+  }
+  TLH_GEMM_CASE(false, false, true)
+  TLH_GEMM_CASE(false, true, true)
+  TLH_GEMM_CASE(true, false, true)
+  TLH_GEMM_CASE(true, true, true)
+  TLH_GEMM_CASE(false, false, false)
+  TLH_GEMM_CASE(false, true, false)
+  TLH_GEMM_CASE(true, false, false)
+  TLH_GEMM_CASE(true, true, false)
+#undef TLH_GEMM_CASE
+}
+
+inline size_t tiles_for(const GemmDesc &d, int bm, int bn) {
+  return size_t((d.M + bm - 1) / bm) * size_t((d.N + bn - 1) / bn);
+}
+
+TileCfg choose_tile(const GemmDesc &d) {
+  const size_t batch = size_t(std::max(1, d.batch));
+  if (tiles_for(d, 128, 128) * batch >= 240) return {128, 128};
+  if (tiles_for(d, 128, 64) * batch >= 240) return {128, 64};
+  if (tiles_for(d, 64, 128) * batch >= 240) return {64, 128};
+  return {64, 64};
+}
+
+bool vec_ok(const GemmDesc &d) {
+  auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int a_contig = d.trans_a ? d.M : d.K;
+  const int b_contig = d.trans_b ? d.K : d.N;
+  if (!al(d.A) || !al(d.B)) return false;
+  if (a_contig % 4 || b_contig % 4 || d.lda % 4 || d.ldb % 4) return false;
+  if (d.batch_ndim > 0) {
+    for (int i = 0; i < d.batch_ndim; ++i)
+      if (d.batch_stride_a[i] % 4 || d.batch_stride_b[i] % 4) return false;
+  }
+  return true;
+}
+
+} // namespace
+
+int gemm_choose_splits(const GemmDesc &d) {
+  if (d.batch > 1 || d.batch_ndim > 0) return 1;
+  const TileCfg t = choose_tile(d);
+  const size_t tiles = tiles_for(d, t.bm, t.bn);
+  if (tiles >= 200 || d.K < 512) return 1;
+  // Aim for ~2 waves of blocks over 256 CUs with K chunks of >= 128.
+  int splits = int((512 + tiles - 1) / tiles);
+  splits = std::min(splits, d.K / 128);
+  splits = std::max(1, std::min(splits, 64));
+  return splits;
+}
+
+size_t gemm_workspace_elems(const GemmDesc &d) {
+  const int s = gemm_choose_splits(d);
+  return s > 1 ? size_t(s) * d.M * d.N : 0;
+}
+
+int gemm_launch(const GemmDesc &d, void *stream) {
+  if (d.M <= 0 || d.N <= 0) return 0;
+  if (d.K <= 0) {
+    // Empty reduction: C = epilogue(0); handled by the split-K reducer path
+    // with zero splits worth of partials.
+  }
+  hipStream_t s = as_stream(stream);
+  GemmParams p{};
+  p.A = d.A; p.B = d.B; p.C = d.C;
+  p.bias = d.bias; p.residual = d.residual; p.aux = d.aux;
+  p.workspace = d.workspace;
+  p.M = d.M; p.N = d.N; p.K = d.K;
+  p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc;
+  p.beta = d.beta;
+  p.epilogue = d.epilogue;
+  p.remap_t = d.remap_t; p.remap_h = d.remap_h; p.remap_d = d.remap_d;
+  p.batch_ndim = d.batch_ndim;
+  for (int i = 0; i < 4; ++i) {
+    p.batch_shape[i] = d.batch_shape[i];
+    p.bsa[i] = d.batch_stride_a[i];
+    p.bsb[i] = d.batch_stride_b[i];
+    p.bsc[i] = d.batch_stride_c[i];
+  }
+  const TileCfg t = choose_tile(d);
+  p.tiles_n = (d.N + t.bn - 1) / t.bn;
+  const int tiles_m = (d.M + t.bm - 1) / t.bm;
+  p.splits = (d.splits > 1 && d.workspace) ? d.splits : 1;
+  if (p.splits > 1 && (d.batch > 1 || d.batch_ndim > 0)) return int(hipErrorInvalidValue);
+  p.k_chunk = p.splits > 1 ? ((d.K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : d.K;
+  if (p.splits > 1) p.splits = (d.K + p.k_chunk - 1) / p.k_chunk;
+  if (d.K <= 0) {
+    // Nothing to accumulate: run the reducer over zero partials.
+    p.splits = 0;
+    gemm_splitk_reduce<<<stride_grid(size_t(d.M) * d.N, 256), 256, 0, s>>>(p);
+    return launch_status();
+  }
+  const int z = p.splits > 1 ? p.splits : std::max(1, d.batch);
+  dim3 grid(unsigned(tiles_m * p.tiles_n), 1, unsigned(z));
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0, vec = vec_ok(d);
+  if (t.bm == 128 && t.bn == 128) launch_cfg<128, 128, 64, 64>(p, ta, tb, vec, grid, s);
+  else if (t.bm == 128 && t.bn == 64) launch_cfg<128, 64, 64, 32>(p, ta, tb, vec, grid, s);
+  else if (t.bm == 64 && t.bn == 128) launch_cfg<64, 128, 32, 64>(p, ta, tb, vec, grid, s);
+  else launch_cfg<64, 64, 32, 32>(p, ta, tb, vec, grid, s);
+  int st = launch_status();
+  if (st) return st;
+  if (p.splits > 1) {
+    gemm_splitk_reduce<<<stride_grid(size_t(d.M) * d.N, 256), 256, 0, s>>>(p);
+    st = launch_status();
+  }
+  return st;
+}
+
+} // namespace tlh
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+#include "../../include/templit_hip.h"
+
+namespace {
+tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
+  tlh::GemmDesc d;
+  d.A = c.a; d.B = c.b; d.C = c.c;
+  d.bias = c.bias; d.residual = c.residual; d.aux = c.aux;
+  d.workspace = c.workspace;
+  d.M = c.m; d.N = c.n; d.K = c.k;
+  d.lda = c.lda; d.ldb = c.ldb; d.ldc = c.ldc;
+  d.trans_a = c.trans_a; d.trans_b = c.trans_b;
+  d.beta = c.beta;
+  d.epilogue = c.epilogue;
+  d.remap_t = c.remap_t; d.remap_h = c.remap_h; d.remap_d = c.remap_d;
+  return d;
+}
+} // namespace
+
+TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
+  if (!desc) return int(hipErrorInvalidValue);
+  tlh::GemmDesc d = from_c(*desc);
+  if (d.M < 0 || d.N < 0 || d.K < 0) return int(hipErrorInvalidValue);
+  if ((d.epilogue == tlh::kEpiGelu || d.epilogue == tlh::kEpiGeluBwd) && !d.aux)
+    return int(hipErrorInvalidValue);
+  if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 || d.M % d.remap_t ||
+                        d.N != d.remap_h * d.remap_d))
+    return int(hipErrorInvalidValue);
+  d.splits = d.workspace ? tlh::gemm_choose_splits(d) : 1;
+  return tlh::gemm_launch(d, stream);
+}
+
+TLH_API int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems) {
+  if (!desc || !elems) return int(hipErrorInvalidValue);
+  *elems = tlh::gemm_workspace_elems(from_c(*desc));
+  return 0;
+}
+
+TLH_API int tlh_matmul(const float *a, const float *b, float *c, uint32_t M,
+                       uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
+                       uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
+                       uint32_t batch_ndim, const uint32_t *batch_shape,
+                       const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                       const uint32_t *batch_stride_c, void *stream) {
+  if (batch_ndim > 4 || c_cs != 1) return int(hipErrorInvalidValue);
+  if (M == 0 || N == 0) return 0;
+  tlh::GemmDesc d;
+  d.A = a; d.B = b; d.C = c;
+  d.M = int(M); d.N = int(N); d.K = int(K);
+  // A: row-major (column stride 1) or column-major (row stride 1).
+  if (a_cs == 1 || K == 1) { d.trans_a = 0; d.lda = int(a_cs == 1 ? a_rs : 1); }
+  else if (a_rs == 1 || M == 1) { d.trans_a = 1; d.lda = int(a_cs); }
+  else return int(hipErrorInvalidValue);
+  if (b_cs == 1 || N == 1) { d.trans_b = 0; d.ldb = int(b_cs == 1 ? b_rs : 1); }
+  else if (b_rs == 1 || K == 1) { d.trans_b = 1; d.ldb = int(b_cs); }
+  else return int(hipErrorInvalidValue);
+  if (d.trans_a == 0 && K == 1) d.lda = int(a_rs);
+  d.ldc = int(c_rs);
+  size_t batch = 1;
+  d.batch_ndim = int(batch_ndim);
+  for (uint32_t i = 0; i < batch_ndim; ++i) {
+    d.batch_shape[i] = batch_shape[i];
+    d.batch_stride_a[i] = batch_stride_a[i];
+    d.batch_stride_b[i] = batch_stride_b[i];
+    d.batch_stride_c[i] = batch_stride_c[i];
+    batch *= batch_shape[i];
+  }
+  if (batch == 0) return 0;
+  if (batch > 65535) return int(hipErrorInvalidValue);
+  d.batch = int(batch);
+  // Collapse a batch whose right operand is shared (stride 0 on every batch
+  // dim) and whose left operand and output are packed row-major into one
+  // tall GEMM with batch*M rows (the weight-broadcast case of nn::Layer).
+  bool b_shared = true, packed = (d.trans_a == 0);
+  size_t expect = size_t(M);
+  for (int i = int(batch_ndim) - 1; i >= 0; --i) {
+    if (batch_shape[i] == 1) continue;
+    if (batch_stride_b[i] != 0) b_shared = false;
+    if (size_t(batch_stride_a[i]) != expect * size_t(d.lda) ||
+        size_t(batch_stride_c[i]) != expect * d.ldc)
+      packed = false;
+    expect *= batch_shape[i];
+  }
+  if (batch > 1 && b_shared && packed && size_t(d.lda) == K && size_t(d.ldc) == N &&
+      batch * M <= 0x7fffffffu) {
+    d.M = int(batch * M);
+    d.batch = 1;
+    d.batch_ndim = 0;
+  }
+  if (d.batch == 1) d.batch_ndim = 0;
+  return tlh::gemm_launch(d, stream);
+}
