@@ -9,8 +9,11 @@
  * entry point taking plain device pointers, sizes and a stream:
  *
  *   - every function returns an int: a hipError_t code, 0 on success;
- *   - pointers are device pointers unless named host_*; they are borrowed
- *     only for the work enqueued by the call;
+ *   - data pointers are device pointers unless named host_*; they are
+ *     borrowed only for the work enqueued by the call. Shape and stride
+ *     arrays (`*_shape`, `*_strides`, `stride_*`, `batch_*`) are host arrays
+ *     read before the call returns. Pointer/size tables of the multi-tensor
+ *     entry points are device arrays (so a captured graph can replay them);
  *   - `stream` is a hipStream_t (NULL = the legacy default stream);
  *   - work is enqueued asynchronously in call order on `stream` (the Metal
  *     runtime's single serial compute encoder, runtime.cpp:290-317);
@@ -214,11 +217,16 @@ int tlh_argmax_rows(const float *a, size_t rows, uint32_t cols,
  * runtime.cpp:1083-1101): *squared_norm += sum(g^2). */
 int tlh_accumulate_gradient_squared_norm(const float *g, size_t n,
                                          float *squared_norm, void *stream);
-/* Multi-tensor version: one launch over `count` tensors (device arrays of
- * pointers and sizes); *squared_norm += sum over all. */
+/* Multi-tensor version (Compiled::step(max_norm)'s loop over every gradient,
+ * include/passes/compile.h:241-245, in one launch): *squared_norm = sum over
+ * `count` tensors of g^2. grads / sizes are device arrays; `partials` is
+ * device scratch of TLH_NORM_PARTIALS floats. Deterministic (fixed
+ * reduction order, no atomics). */
+#define TLH_NORM_PARTIALS 1024
 int tlh_gradient_squared_norm_multi(const float *const *grads,
                                     const uint64_t *sizes, uint32_t count,
-                                    float *squared_norm, void *stream);
+                                    float *partials, float *squared_norm,
+                                    void *stream);
 /* Column sums: out[c] (+)= sum_r a[r, c]  (bias gradients, the
  * sum_to_shape [.., N] -> [1, N] case). beta scales the old out. */
 int tlh_column_sum(const float *a, size_t rows, uint32_t cols, float *out,
@@ -247,6 +255,12 @@ int tlh_cross_entropy_rows(const float *logits, const uint32_t *targets,
 int tlh_cross_entropy_rows_backward(const float *logits, const uint32_t *targets,
                                     float *grad, size_t rows, uint32_t vocab,
                                     const float *row_scale, void *stream);
+/* Fused forward + backward in one pass over the logits: losses as
+ * tlh_cross_entropy_rows, grad as tlh_cross_entropy_rows_backward times
+ * `scale` (the uniform root gradient 1/(B*T) of src/train.cpp:109-113). */
+int tlh_cross_entropy_rows_fused(const float *logits, const uint32_t *targets,
+                                 float *losses, float *grad, size_t rows,
+                                 uint32_t vocab, float scale, void *stream);
 /* RMS (runtime.cpp:1031-1052): rms[r] = sqrt(sum(x^2)/cols + eps). */
 int tlh_rms(const float *x, float *rms, size_t rows, uint32_t cols, float eps,
             void *stream);
@@ -283,18 +297,6 @@ int tlh_embedding_add_positions(const float *tok, const float *pos,
  * pre-fills dst (base copy or zero, runtime.cpp:983-1030). */
 int tlh_scatter_add_rows(const float *values, const uint32_t *ids, size_t n_ids,
                          uint32_t dim, float *dst, void *stream);
-/* Deterministic embedding backward: dst[r,:] = beta*dst[r,:] + sum over i
- * with ids[i]==r of values[i,:] in increasing i. `order` / `offsets` come
- * from tlh_sort_ids (scratch of n_ids + rows + 1 uint32). */
-int tlh_scatter_rows_sorted(const float *values, const uint32_t *order,
-                            const uint32_t *offsets, uint32_t rows,
-                            uint32_t dim, float *dst, float beta, void *stream);
-/* Stable counting sort of ids into order[n_ids] and offsets[rows+1]
- * (device scratch `counts` of rows+1 uint32). */
-int tlh_sort_ids(const uint32_t *ids, size_t n_ids, uint32_t rows,
-                 uint32_t *order, uint32_t *offsets, uint32_t *counts,
-                 void *stream);
-
 /* ---------------------------------------------------------------------------
  * Attention (no reference op: replaces the decomposed chain of
  * include/nn/multi_head.h:33-55)

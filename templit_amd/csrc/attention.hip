@@ -1,0 +1,472 @@
+// Fused causal multi-head attention, forward and backward, on fp32 MFMA.
+//
+// No reference kernel: the reference builds attention from ~14 runtime calls
+// per block (include/nn/multi_head.h:37-52): split_last_dim + transpose for
+// Q/K/V, a transpose of K, a batched matmul, divide by sqrt(64), add the
+// causal mask (include/nn/attention.h:9-22), softmax, matmul with V,
+// transpose + merge_last_dims -- materialising [B,H,T,T] scores twice.
+// Here each wave keeps 32 query (or key) rows in registers and streams
+// 64-row K/V (or Q/dO) tiles through LDS; scores never reach HBM.
+//
+// MFMA v_mfma_f32_32x32x2f32, 64 lanes, r = lane%32, h = lane/32:
+//   A operand: A[m=r][k-slot h];  B operand: B[k-slot h][n=r];
+//   accumulator reg v: D[m = 8*(v/4) + 4*h + v%4][n = r].
+// The forward computes S^T = K.Q^T (m = key, n = query). Its accumulator
+// holds, per lane, keys key(v,h) = 8*(v/4)+4h+v%4 of query r -- exactly the
+// B-operand layout P^T needs for O^T = V^T.P^T when step s uses k-slot key
+// key(s,h). So P never leaves the registers. The backward uses the same
+// identity in both directions.
+#include "common.h"
+
+#include "../../include/templit_hip.h"
+
+using namespace tlh;
+
+namespace {
+
+constexpr int HD = 64;       // head dim
+constexpr int LDP = HD + 4;  // padded LDS row (floats)
+constexpr int KB = 64;       // rows per streamed LDS tile
+constexpr int WQ = 32;       // rows per wave
+constexpr int BQ = 4 * WQ;   // rows per block
+
+struct Dims {
+  uint32_t B, H, T;
+};
+
+// element offset of (b, h, t, 0) in head layout [B,H,T,D] or merged [B,T,H*D]
+__device__ inline size_t row_off(const Dims &d, uint32_t b, uint32_t h, uint32_t t, int merged) {
+  return merged ? ((size_t(b) * d.T + t) * d.H + h) * HD : ((size_t(b) * d.H + h) * d.T + t) * HD;
+}
+
+__device__ inline int key_of(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
+
+__device__ inline f16x mfma(float a, float b, const f16x &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Cooperative load of rows [r0, r0+64) of a [T, 64] head matrix into an LDS
+// tile with row stride LDP; rows >= T are zero.
+__device__ inline void load_tile(float *tile, const float *src_base, const Dims &d, uint32_t b,
+                                 uint32_t h, int r0, int merged) {
+  // 64 rows x 16 float4 = 1024 float4, 4 per thread.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = threadIdx.x + i * 256;
+    const int row = idx >> 4, c4 = idx & 15;
+    const int t = r0 + row;
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (t < int(d.T)) v = *reinterpret_cast<const f4 *>(src_base + row_off(d, b, h, t, merged) + c4 * 4);
+    *reinterpret_cast<f4 *>(tile + row * LDP + c4 * 4) = v;
+  }
+}
+
+// Loads 32 consecutive head-dim values (dims 32*hh .. +31) of row t into regs.
+__device__ inline void load_row_half(float (&reg)[32], const float *src, bool valid) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = *reinterpret_cast<const f4 *>(src + i * 4);
+    reg[4 * i] = v.x; reg[4 * i + 1] = v.y; reg[4 * i + 2] = v.z; reg[4 * i + 3] = v.w;
+  }
+}
+
+// Writes each wave's 32x64 result, held transposed in MFMA accumulators
+// (acc[dt][v] = X[row r][dim 32dt + key_of(v,h)]), through LDS so that the
+// global stores are row-contiguous float4s. Called by every wave of the
+// block (it contains barriers); rows >= T are not stored.
+__device__ inline void store_rows_via_lds(float *smem, const f16x (&acc)[2], float mul,
+                                          float *dst_base, const Dims &d, uint32_t b,
+                                          uint32_t h, int row0, int merged, int lane, int wave) {
+  float *wave_lds = smem + wave * WQ * LDP;
+  const int r = lane & 31, hh = lane >> 5;
+  __syncthreads();
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) wave_lds[r * LDP + 32 * dt + key_of(v, hh)] = acc[dt][v] * mul;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = i * 4 + (lane >> 4), c4 = lane & 15;
+    const int t = row0 + row;
+    if (t < int(d.T)) {
+      const f4 v = *reinterpret_cast<const f4 *>(wave_lds + row * LDP + c4 * 4);
+      *reinterpret_cast<f4 *>(dst_base + row_off(d, b, h, t, merged) + c4 * 4) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__ q,
+                                                       const float *__restrict__ k,
+                                                       const float *__restrict__ v,
+                                                       float *__restrict__ o,
+                                                       float *__restrict__ lse, Dims d,
+                                                       float scale, int causal, int o_merged) {
+  __shared__ __attribute__((aligned(16))) float smem[2 * KB * LDP];
+  float *Ks = smem;
+  float *Vs = smem + KB * LDP;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, hh = lane >> 5;
+  const uint32_t bh = blockIdx.y;
+  const uint32_t b = bh / d.H, h = bh % d.H;
+  const int q_block = blockIdx.x * BQ;
+  const int q0 = q_block + wave * WQ;
+  const int my_q = q0 + r;
+  const bool active = q0 < int(d.T);
+
+  float qreg[32];
+  load_row_half(qreg, q + row_off(d, b, h, my_q < int(d.T) ? my_q : 0, 0) + 32 * hh,
+                my_q < int(d.T));
+
+  f16x oacc[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int q_end = min(int(d.T), q_block + BQ);
+  const int k_end = causal ? q_end : int(d.T);
+  const int nkb = (k_end + KB - 1) / KB;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * KB;
+    __syncthreads();
+    load_tile(Ks, k, d, b, h, k0, 0);
+    load_tile(Vs, v, d, b, h, k0, 0);
+    __syncthreads();
+    if (!active || (causal && k0 > q0 + WQ - 1)) continue;
+    f16x st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[mt][i] = 0.f;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      f4 ka[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        ka[mt] = *reinterpret_cast<const f4 *>(Ks + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) st[mt] = mfma(ka[mt][j], qreg[4 * s4 + j], st[mt]);
+    }
+    // scale, mask, online softmax (per query = r; keys spread over v, mt, h)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = k0 + 32 * mt + key_of(i, hh);
+        float sv = st[mt][i] * scale;
+        if (key >= int(d.T) || (causal && key > my_q)) sv = -INFINITY;
+        st[mt][i] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = expf(st[mt][i] - m_use);
+        st[mt][i] = p;
+        ps += p;
+      }
+    ps += __shfl_xor(ps, 32, 64);
+    const float alpha = expf(m_run - m_use);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+    // O^T += V^T . P^T ; step s -> (mt, i) = (s/16, s%16), key = 32mt + key_of(i, hh)
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      const int mt = s >> 4, i = s & 15;
+      const int key = 32 * mt + key_of(i, hh);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+        oacc[dt] = mfma(Vs[key * LDP + 32 * dt + r], st[mt][i], oacc[dt]);
+    }
+  }
+  // epilogue: O = O / l ; lse = m + log(l)
+  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  if (active && hh == 0 && my_q < int(d.T))
+    lse[(size_t(b) * d.H + h) * d.T + my_q] = m_run + logf(l_run);
+  store_rows_via_lds(smem, oacc, inv_l, o, d, b, h, q0, o_merged, lane, wave);
+}
+
+// delta[b,h,t] = sum_d dO[t,d] * O[t,d]
+__global__ __launch_bounds__(256) void attn_delta_kernel(const float *__restrict__ o,
+                                                         const float *__restrict__ dout,
+                                                         float *__restrict__ delta, Dims d,
+                                                         int merged) {
+  const int lane = threadIdx.x & 63;
+  const size_t rows = size_t(d.B) * d.H * d.T;
+  for (size_t row = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6; row < rows;
+       row += (size_t(gridDim.x) * blockDim.x) >> 6) {
+    const uint32_t t = uint32_t(row % d.T);
+    const uint32_t bh = uint32_t(row / d.T);
+    const size_t off = row_off(d, bh / d.H, bh % d.H, t, merged);
+    float x = o[off + lane] * dout[off + lane];
+    x = wave_sum(x);
+    if (lane == 0) delta[row] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, part 1: dK, dV. Each wave owns 32 keys; query tiles stream
+// through LDS. S = Q.K^T is computed with m = query, n = key, so a lane holds
+// queries q(v,h) of key r: the A-operand layout of P^T / dS^T for
+// dV = P^T.dO and dK = dS^T.Q.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_bwd_kv_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv, Dims d,
+    float scale, int causal, int o_merged, int dqkv_merged) {
+  __shared__ __attribute__((aligned(16))) float smem[2 * KB * LDP + 2 * KB];
+  float *Qs = smem;
+  float *dOs = smem + KB * LDP;
+  float *lse_s = smem + 2 * KB * LDP;
+  float *delta_s = lse_s + KB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, hh = lane >> 5;
+  const uint32_t bh = blockIdx.y;
+  const uint32_t b = bh / d.H, h = bh % d.H;
+  const int k_block = blockIdx.x * BQ;
+  const int key0 = k_block + wave * WQ;
+  const int my_key = key0 + r;
+  const bool active = key0 < int(d.T);
+
+  float kreg[32], vreg[32];
+  const bool kvalid = my_key < int(d.T);
+  const size_t koff = row_off(d, b, h, kvalid ? my_key : 0, 0) + 32 * hh;
+  load_row_half(kreg, k + koff, kvalid);
+  load_row_half(vreg, v + koff, kvalid);
+
+  f16x dk_acc[2], dv_acc[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      dk_acc[dt][i] = 0.f;
+      dv_acc[dt][i] = 0.f;
+    }
+
+  const size_t lse_base = (size_t(b) * d.H + h) * d.T;
+  const int q_start = causal ? (k_block / KB) * KB : 0;
+  for (int qt0 = q_start; qt0 < int(d.T); qt0 += KB) {
+    __syncthreads();
+    load_tile(Qs, q, d, b, h, qt0, 0);
+    load_tile(dOs, dout, d, b, h, qt0, o_merged);
+    if (threadIdx.x < KB) {
+      const int t = qt0 + threadIdx.x;
+      lse_s[threadIdx.x] = t < int(d.T) ? lse[lse_base + t] : 0.f;
+      delta_s[threadIdx.x] = t < int(d.T) ? delta[lse_base + t] : 0.f;
+    }
+    __syncthreads();
+    if (!active || (causal && qt0 + KB - 1 < key0)) continue;
+    // S[q][key] for 64 queries (mt) x 32 keys
+    f16x sp[2], dp[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sp[mt][i] = 0.f;
+        dp[mt][i] = 0.f;
+      }
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      f4 qa[2], da[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        qa[mt] = *reinterpret_cast<const f4 *>(Qs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+        da[mt] = *reinterpret_cast<const f4 *>(dOs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          sp[mt] = mfma(qa[mt][j], kreg[4 * s4 + j], sp[mt]);
+          dp[mt] = mfma(da[mt][j], vreg[4 * s4 + j], dp[mt]);
+        }
+    }
+    // P = exp(S*scale - lse[q]) masked; dS = P * (dP - delta[q])
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ql = 32 * mt + key_of(i, hh);
+        const int qq = qt0 + ql;
+        float p = expf(sp[mt][i] * scale - lse_s[ql]);
+        if (qq >= int(d.T) || my_key >= int(d.T) || (causal && my_key > qq)) p = 0.f;
+        sp[mt][i] = p;
+        dp[mt][i] = p * (dp[mt][i] - delta_s[ql]);
+      }
+    // dV[key][dim] += P^T . dO ; dK[key][dim] += dS^T . Q
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      const int mt = s >> 4, i = s & 15;
+      const int ql = 32 * mt + key_of(i, hh);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        dv_acc[dt] = mfma(sp[mt][i], dOs[ql * LDP + 32 * dt + r], dv_acc[dt]);
+        dk_acc[dt] = mfma(dp[mt][i], Qs[ql * LDP + 32 * dt + r], dk_acc[dt]);
+      }
+    }
+  }
+  if (!active) return;
+  // accumulators: D[m = key key_of(v,h)][n = dim r + 32dt] -> row-contiguous stores
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = key0 + key_of(i, hh);
+      if (key < int(d.T)) {
+        const size_t off = row_off(d, b, h, key, dqkv_merged) + 32 * dt + r;
+        dk[off] = dk_acc[dt][i] * scale;
+        dv[off] = dv_acc[dt][i];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward, part 2: dQ. Each wave owns 32 queries; K/V tiles stream through
+// LDS (as in the forward). dQ^T = K^T.dS^T uses dS^T straight from the
+// S^T-layout registers as the B operand.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_bwd_q_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dq, Dims d, float scale, int causal,
+    int o_merged, int dqkv_merged) {
+  __shared__ __attribute__((aligned(16))) float smem[2 * KB * LDP];
+  float *Ks = smem;
+  float *Vs = smem + KB * LDP;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, hh = lane >> 5;
+  const uint32_t bh = blockIdx.y;
+  const uint32_t b = bh / d.H, h = bh % d.H;
+  const int q_block = blockIdx.x * BQ;
+  const int q0 = q_block + wave * WQ;
+  const int my_q = q0 + r;
+  const bool active = q0 < int(d.T);
+  const bool qvalid = my_q < int(d.T);
+
+  float qreg[32], doreg[32];
+  load_row_half(qreg, q + row_off(d, b, h, qvalid ? my_q : 0, 0) + 32 * hh, qvalid);
+  load_row_half(doreg, dout + row_off(d, b, h, qvalid ? my_q : 0, o_merged) + 32 * hh, qvalid);
+  const size_t lse_base = (size_t(b) * d.H + h) * d.T;
+  const float my_lse = qvalid ? lse[lse_base + my_q] : 0.f;
+  const float my_delta = qvalid ? delta[lse_base + my_q] : 0.f;
+
+  f16x dq_acc[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dq_acc[dt][i] = 0.f;
+
+  const int q_end = min(int(d.T), q_block + BQ);
+  const int k_end = causal ? q_end : int(d.T);
+  const int nkb = (k_end + KB - 1) / KB;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * KB;
+    __syncthreads();
+    load_tile(Ks, k, d, b, h, k0, 0);
+    load_tile(Vs, v, d, b, h, k0, 0);
+    __syncthreads();
+    if (!active || (causal && k0 > q0 + WQ - 1)) continue;
+    f16x st[2], dpt[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        st[mt][i] = 0.f;
+        dpt[mt][i] = 0.f;
+      }
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      f4 ka[2], va[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        ka[mt] = *reinterpret_cast<const f4 *>(Ks + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+        va[mt] = *reinterpret_cast<const f4 *>(Vs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          st[mt] = mfma(ka[mt][j], qreg[4 * s4 + j], st[mt]);
+          dpt[mt] = mfma(va[mt][j], doreg[4 * s4 + j], dpt[mt]);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = k0 + 32 * mt + key_of(i, hh);
+        float p = expf(st[mt][i] * scale - my_lse);
+        if (!qvalid || key >= int(d.T) || (causal && key > my_q)) p = 0.f;
+        dpt[mt][i] = p * (dpt[mt][i] - my_delta);
+      }
+    // dQ^T[dim][q] += K^T[dim][key] . dS^T[key][q]
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      const int mt = s >> 4, i = s & 15;
+      const int key = 32 * mt + key_of(i, hh);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+        dq_acc[dt] = mfma(Ks[key * LDP + 32 * dt + r], dpt[mt][i], dq_acc[dt]);
+    }
+  }
+  store_rows_via_lds(smem, dq_acc, scale, dq, d, b, h, q0, dqkv_merged, lane, wave);
+}
+
+} // namespace
+
+TLH_API int tlh_attention_forward(const float *q, const float *k, const float *v, float *o,
+                                  float *lse, uint32_t batch, uint32_t heads, uint32_t seq,
+                                  uint32_t head_dim, float scale, int causal, int o_merged,
+                                  void *stream) {
+  if (head_dim != HD) return int(hipErrorInvalidValue);
+  if (size_t(batch) * heads * seq == 0) return 0;
+  if (size_t(batch) * heads > 65535) return int(hipErrorInvalidValue);
+  const Dims d{batch, heads, seq};
+  dim3 grid(ceil_div(seq, BQ), batch * heads);
+  attn_fwd_kernel<<<grid, 256, 0, as_stream(stream)>>>(q, k, v, o, lse, d, scale, causal,
+                                                       o_merged);
+  return launch_status();
+}
+
+TLH_API int tlh_attention_backward(const float *q, const float *k, const float *v,
+                                   const float *o, const float *do_, const float *lse,
+                                   float *delta, float *dq, float *dk, float *dv,
+                                   uint32_t batch, uint32_t heads, uint32_t seq,
+                                   uint32_t head_dim, float scale, int causal, int o_merged,
+                                   int dqkv_merged, void *stream) {
+  if (head_dim != HD) return int(hipErrorInvalidValue);
+  if (size_t(batch) * heads * seq == 0) return 0;
+  if (size_t(batch) * heads > 65535) return int(hipErrorInvalidValue);
+  hipStream_t s = as_stream(stream);
+  const Dims d{batch, heads, seq};
+  const size_t rows = size_t(batch) * heads * seq;
+  attn_delta_kernel<<<stride_grid(rows * 64, 256), 256, 0, s>>>(o, do_, delta, d, o_merged);
+  int st = launch_status();
+  if (st) return st;
+  dim3 grid(ceil_div(seq, BQ), batch * heads);
+  attn_bwd_kv_kernel<<<grid, 256, 0, s>>>(q, k, v, do_, lse, delta, dk, dv, d, scale, causal,
+                                          o_merged, dqkv_merged);
+  if ((st = launch_status())) return st;
+  attn_bwd_q_kernel<<<grid, 256, 0, s>>>(q, k, v, do_, lse, delta, dq, d, scale, causal,
+                                         o_merged, dqkv_merged);
+  return launch_status();
+}

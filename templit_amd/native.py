@@ -93,13 +93,14 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_argmax": [P, c_size_t, P, P],
     "tlh_argmax_rows": [P, c_size_t, c_uint32, P, P],
     "tlh_accumulate_gradient_squared_norm": [P, c_size_t, P, P],
-    "tlh_gradient_squared_norm_multi": [P, P, c_uint32, P, P],
+    "tlh_gradient_squared_norm_multi": [P, P, c_uint32, P, P, P],
     "tlh_column_sum": [P, c_size_t, c_uint32, P, c_float, P],
     # row ops
     "tlh_softmax": [P, P, c_size_t, c_uint32, P],
     "tlh_softmax_backward": [P, P, P, c_size_t, c_uint32, P],
     "tlh_cross_entropy_rows": [P, P, P, c_size_t, c_uint32, P],
     "tlh_cross_entropy_rows_backward": [P, P, P, c_size_t, c_uint32, P, P],
+    "tlh_cross_entropy_rows_fused": [P, P, P, P, c_size_t, c_uint32, c_float, P],
     "tlh_rms": [P, P, c_size_t, c_uint32, c_float, P],
     "tlh_rms_norm": [P, P, P, P, c_size_t, c_uint32, c_float, P],
     "tlh_rms_norm_backward": [P, P, P, P, P, c_size_t, c_uint32, c_float, c_float, P],
@@ -107,8 +108,6 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_embedding_lookup": [P, c_uint32, c_uint32, P, c_size_t, P, P],
     "tlh_embedding_add_positions": [P, P, P, c_uint32, c_uint32, c_uint32, P, P],
     "tlh_scatter_add_rows": [P, P, c_size_t, c_uint32, P, P],
-    "tlh_scatter_rows_sorted": [P, P, P, c_uint32, c_uint32, P, c_float, P],
-    "tlh_sort_ids": [P, c_size_t, c_uint32, P, P, P, P],
     # attention
     "tlh_attention_forward": [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32,
                               c_float, c_int, c_int, P],

@@ -1,0 +1,530 @@
+"""Parity of every C-ABI kernel entry point with the CPU oracle, on seeded
+inputs, at the benchmark's shapes where the oracle is fast enough and at the
+reference's edge cases (ragged sizes, broadcasting, ties, invalid targets,
+in-place use). Tolerances: rtol 1e-4 / atol 1e-5 for elementwise and
+reduction ops, 1e-3 relative for matmul and attention, bit-exact for
+gathers and argmax.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_util import Gpu, assert_close, assert_rel, u32
+from templit_amd.native import EPI_GELU, EPI_GELU_BWD, GemmDesc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def g():
+    return Gpu()
+
+
+# ---------------------------------------------------------------------------
+# elementwise
+# ---------------------------------------------------------------------------
+BROADCASTS = [
+    ((6144, 384), (6144, 384)),          # same shape
+    ((6144, 384), (1, 384)),             # bias row
+    ((32, 6, 192, 192), (1, 1, 192, 192)),  # causal mask
+    ((32, 6, 192, 192), (1, 1)),         # divide by sqrt(64)
+    ((32, 192, 384), (32, 192, 1)),      # RMSNorm' column broadcast
+    ((32, 192, 1), (32, 192, 2048)),     # CE upstream scale
+    ((2, 3), (3,)),                      # rank mismatch (test_metal_runtime.cpp:160)
+    ((5, 1, 7), (1, 3, 1)),              # both broadcast
+    ((3, 1, 4, 1, 2), (1, 5, 1, 6, 2)),  # generic rank-5 decode
+]
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "hadamard", "divide"])
+@pytest.mark.parametrize("sa,sb", BROADCASTS)
+def test_binary_broadcast(g, op, sa, sb):
+    a = O.normal(sa, 1, 0, 1)
+    b = O.normal(sb, 2, 3, 1)
+    out_shape = O.broadcast_shape(sa, sb)
+    expect = O.binary(op, a, b)
+    da, db, do = g.dev(a), g.dev(b), g.empty(out_shape)
+    g.call(f"tlh_{op}", da, db, do, len(out_shape), u32(out_shape),
+           u32(O.broadcast_strides(sa, out_shape)), u32(O.broadcast_strides(sb, out_shape)))
+    assert_close(g.host(do), expect, what=op)
+
+
+def test_binary_in_place(g):
+    # LINEAR's add(destination, bias, destination) (execute.h:249)
+    a = O.normal((512, 384), 3)
+    b = O.normal((1, 384), 4)
+    expect = O.binary("add", a, b)
+    da, db = g.dev(a), g.dev(b)
+    g.call("tlh_add", da, db, da, 2, u32([512, 384]), u32([384, 1]), u32([0, 1]))
+    assert_close(g.host(da), expect)
+
+
+@pytest.mark.parametrize("name,orc,pos", [("sqrt", "sqrt", True), ("exp", "exp", False),
+                                         ("sigmoid", "sigmoid", False), ("gelu", "gelu", False),
+                                         ("gelu_derivative", "gelu_derivative", False),
+                                         ("copy", "copy", False)])
+@pytest.mark.parametrize("n", [1, 1023, 6144 * 1536])
+def test_unary(g, name, orc, pos, n):
+    x = O.normal((n,), 5, 0, 2)
+    if pos:
+        x = np.abs(x)
+    out = g.empty((n,))
+    g.call(f"tlh_{name}", g.dev(x), out, n)
+    assert_close(g.host(out), O.unary(orc, x), what=name)
+
+
+@pytest.mark.parametrize("name,orc,s", [("add_scalar", "add", 1e-6), ("divide_scalar", "divide", 384.0),
+                                       ("pow_scalar", "pow", 3.0)])
+def test_scalar_ops(g, name, orc, s):
+    x = np.abs(O.normal((100003,), 6)) + 0.1
+    out = g.empty(x.shape)
+    g.call(f"tlh_{name}", g.dev(x), s, out, x.size)
+    assert_close(g.host(out), O.scalar(orc, x, s), what=name)
+
+
+def test_gelu_backward(g):
+    x = O.normal((6144 * 1536 + 3,), 7, 0, 2)
+    gr = O.normal(x.shape, 8)
+    out = g.empty(x.shape)
+    g.call("tlh_gelu_backward", g.dev(gr), g.dev(x), out, x.size)
+    expect = O.binary("hadamard", gr, O.unary("gelu_derivative", x))
+    assert_close(g.host(out), expect)
+
+
+TRANSPOSES = [((6144, 1536), -2, -1), ((32, 192, 6, 64), 1, 2), ((32, 6, 192, 64), -2, -1),
+              ((4, 100, 70), -2, -1), ((3, 4, 5, 6), 0, 3), ((1, 384), 0, 1)]
+
+
+@pytest.mark.parametrize("shape,da,db", TRANSPOSES)
+def test_transpose(g, shape, da, db):
+    x = O.normal(shape, 9)
+    expect = O.transpose(x, da, db)
+    nd = len(shape)
+    a, b = da % nd, db % nd
+    ist = O.contiguous_strides(shape)
+    ist[a], ist[b] = ist[b], ist[a]
+    out = g.empty(expect.shape)
+    g.call("tlh_transpose", g.dev(x), out, nd, u32(expect.shape), u32(ist))
+    np.testing.assert_array_equal(g.host(out), expect)  # a permutation is exact
+
+
+# ---------------------------------------------------------------------------
+# matmul
+# ---------------------------------------------------------------------------
+def mult(g, a, b):
+    M, K = a.shape[-2], a.shape[-1]
+    N = b.shape[-1]
+    ab, bb = list(a.shape[:-2]), list(b.shape[:-2])
+    batch = O.broadcast_shape(ab, bb) if (ab or bb) else []
+    sa = [s * M * K for s in O.broadcast_strides(ab, batch)] if ab else [0] * len(batch)
+    sb = [s * K * N for s in O.broadcast_strides(bb, batch)] if bb else [0] * len(batch)
+    sc = [s * M * N for s in O.contiguous_strides(batch)]
+    out = g.empty(batch + [M, N])
+    g.call("tlh_matmul", g.dev(a), g.dev(b), out, M, K, N, K, 1, N, 1, N, 1, len(batch),
+           u32(batch or [1]), u32(sa or [0]), u32(sb or [0]), u32(sc or [0]))
+    return g.host(out)
+
+
+MATMULS = [
+    ((768, 384), (384, 1536)),                 # config 1
+    ((2, 3), (3, 2)),                          # KAT shape
+    ((32, 192, 384), (384, 384)),              # linear, weight broadcast over batch
+    ((32, 6, 192, 64), (32, 6, 64, 192)),      # attention scores
+    ((32, 6, 192, 192), (32, 6, 192, 64)),     # attention output
+    ((32, 384, 192), (32, 192, 384)),          # per-sample weight grad
+    ((2, 1, 33, 17), (1, 3, 17, 29)),          # broadcast both batch dims, ragged
+    ((1, 65), (65, 1)),                        # vector dot
+]
+
+
+@pytest.mark.parametrize("sa,sb", MATMULS)
+def test_matmul(g, sa, sb):
+    a = O.normal(sa, 10, 0, 0.5)
+    b = O.normal(sb, 11, 0, 0.5)
+    assert_rel(mult(g, a, b), O.matmul(a, b), 1e-3, "matmul")
+
+
+def test_matmul_kat_and_identity(g):
+    # test_metal_runtime.cpp:281-342
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    np.testing.assert_allclose(mult(g, a, b), [[58, 64], [139, 154]], atol=1e-5)
+    ident = np.stack([np.eye(64, dtype=np.float32)] * 2)
+    vals = (np.arange(2 * 64 * 64) % 31 - 15).astype(np.float32).reshape(2, 64, 64)
+    np.testing.assert_allclose(mult(g, ident, vals), vals, atol=1e-5)
+
+
+def gemm(g, a, b, ta=False, tb=False, bias=None, residual=None, epi=0, aux=None, beta=0.0,
+         c_init=None, remap=None, split=True):
+    M = a.shape[1] if ta else a.shape[0]
+    K = a.shape[0] if ta else a.shape[1]
+    N = b.shape[0] if tb else b.shape[1]
+    d = GemmDesc()
+    da, db = g.dev(a), g.dev(b)
+    dc = g.dev(c_init) if c_init is not None else g.zeros((M * N,))
+    keep = [da, db, dc]
+    d.a, d.b, d.c = da.data_ptr(), db.data_ptr(), dc.data_ptr()
+    if bias is not None:
+        t = g.dev(bias); keep.append(t); d.bias = t.data_ptr()
+    if residual is not None:
+        t = g.dev(residual); keep.append(t); d.residual = t.data_ptr()
+    daux = None
+    if aux is not None:
+        daux = g.dev(aux); keep.append(daux); d.aux = daux.data_ptr()
+    elif epi == EPI_GELU:
+        daux = g.zeros((M * N,)); keep.append(daux); d.aux = daux.data_ptr()
+    d.m, d.n, d.k = M, N, K
+    d.lda = M if ta else K
+    d.ldb = K if tb else N
+    d.ldc = N
+    d.trans_a, d.trans_b = int(ta), int(tb)
+    d.beta = beta
+    d.epilogue = epi
+    if remap:
+        d.remap_t, d.remap_h, d.remap_d = remap
+    if split:
+        n = ctypes.c_size_t()
+        g.lib.tlh_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n))
+        if n.value:
+            ws = g.empty((n.value,)); keep.append(ws); d.workspace = ws.data_ptr()
+    g.call("tlh_gemm", ctypes.byref(d))
+    return g.host(dc), (g.host(daux) if daux is not None else None)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(6144, 384, 384), (384, 384, 6144), (100, 70, 37)])
+def test_gemm_layouts(g, ta, tb, M, N, K):
+    a = O.normal((K, M) if ta else (M, K), 12, 0, 0.5)
+    b = O.normal((N, K) if tb else (K, N), 13, 0, 0.5)
+    out, _ = gemm(g, a, b, ta, tb)
+    expect = O.matmul(a.T if ta else a, b.T if tb else b)
+    assert_rel(out.reshape(M, N), expect, 1e-3, "gemm")
+
+
+def test_gemm_bias_residual_beta(g):
+    M, N, K = 1000, 384, 384
+    a, b = O.normal((M, K), 14, 0, 0.1), O.normal((K, N), 15, 0, 0.1)
+    bias, res, c0 = O.normal((N,), 16), O.normal((M, N), 17), O.normal((M, N), 18)
+    out, _ = gemm(g, a, b, bias=bias, residual=res, beta=1.0, c_init=c0)
+    expect = O.matmul(a, b) + bias + c0 + res
+    assert_rel(out.reshape(M, N), expect, 1e-3)
+
+
+def test_gemm_gelu_and_gelu_backward(g):
+    M, N, K = 768, 1536, 384
+    a, b = O.normal((M, K), 19, 0, 0.1), O.normal((K, N), 20, 0, 0.1)
+    bias = O.normal((N,), 21, 0, 0.1)
+    out, pre = gemm(g, a, b, bias=bias, epi=EPI_GELU)
+    u = O.binary("add", O.matmul(a, b), bias.reshape(1, N))
+    assert_rel(pre.reshape(M, N), u, 1e-3)
+    assert_rel(out.reshape(M, N), O.unary("gelu", u), 1e-3)
+    # backward epilogue: C = (dY . W^T) * GELU'(u) with W stored [N, K]
+    uu = O.normal((M, N), 24)
+    dy = O.normal((M, K), 25)
+    w = O.normal((N, K), 26, 0, 0.1)
+    out2, _ = gemm(g, dy, w, tb=True, epi=EPI_GELU_BWD, aux=uu)
+    expect = O.binary("hadamard", O.matmul(dy, w.T), O.unary("gelu_derivative", uu))
+    assert_rel(out2.reshape(M, N), expect, 1e-3)
+
+
+def test_gemm_head_remap(g):
+    B, T, H, D = 4, 48, 6, 64
+    a, b = O.normal((B * T, H * D), 27, 0, 0.1), O.normal((H * D, H * D), 28, 0, 0.1)
+    bias = O.normal((H * D,), 29)
+    out, _ = gemm(g, a, b, bias=bias, remap=(T, H, D))
+    y = O.binary("add", O.matmul(a, b), bias.reshape(1, -1)).reshape(B, T, H, D)
+    assert_rel(out.reshape(B, H, T, D), y.transpose(0, 2, 1, 3), 1e-3)
+
+
+# ---------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------
+REDUCTIONS = [
+    ((2, 3), [1, 3]), ((2, 3), [2, 1]), ((2, 3, 4), [1, 3, 1]), ((2, 3, 4), [2, 1, 1]),
+    ((2, 3, 4), [1, 1, 1]), ((2, 3, 4), [4]), ((1, 4), [4]),          # KATs 344-430
+    ((32, 384, 384), [384, 384]), ((32, 192, 384), [1, 384]),        # weight / bias grads
+    ((32, 192, 384), [32, 192, 1]), ((32, 6, 192, 192), [32, 6, 192, 1]),  # sum(axis)
+    ((5, 7, 9, 11), [5, 1, 9, 1]), ((6144, 384), [6144, 384]),      # generic, identity copy
+]
+
+
+@pytest.mark.parametrize("shape,target", REDUCTIONS)
+def test_sum_to_shape(g, shape, target):
+    x = O.normal(shape, 30)
+    al = O.aligned_shape(shape, target)
+    out = g.empty(al)
+    g.call("tlh_sum_to_shape", g.dev(x), out, len(shape), u32(shape), u32(al))
+    assert_close(g.host(out).reshape(target), O.sum_to_shape(x, target), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("shape,target", [((2, 3), [2, 1]), ((32, 6, 192, 192), [32, 6, 192, 1]),
+                                          ((7, 9, 5), [1, 9, 5]), ((4, 5, 6), [4, 1, 6])])
+def test_max_to_shape(g, shape, target):
+    x = O.normal(shape, 31)
+    al = O.aligned_shape(shape, target)
+    out = g.empty(al)
+    g.call("tlh_max_to_shape", g.dev(x), out, len(shape), u32(shape), u32(al))
+    np.testing.assert_array_equal(g.host(out).reshape(target), O.max_to_shape(x, target))
+
+
+@pytest.mark.parametrize("n", [1, 6, 5000, 6144 * 384])
+def test_sum_all(g, n):
+    x = O.normal((n,), 32)
+    out = g.empty((1,))
+    g.call("tlh_sum", g.dev(x), n, out)
+    np.testing.assert_allclose(g.host(out)[0], x.astype(np.float64).sum(), rtol=1e-4, atol=1e-3)
+
+
+def test_argmax_kats(g):
+    # test_metal_runtime.cpp:509-531 + lowest index on ties + -inf/NaN rows
+    cases = [np.array([1, 4, 2, 9, 3, 5], np.float32)]
+    big = np.zeros(5000, np.float32); big[4097] = 100; cases.append(big)
+    ties = np.zeros(3000, np.float32); ties[[17, 500, 2999]] = 7; cases.append(ties)
+    cases.append(np.full(300, -np.inf, np.float32))
+    nan = O.normal((2048,), 33); nan[5] = np.nan; cases.append(nan)
+    for x in cases + [O.normal((2048,), 34), O.normal((6144 * 2048,), 35)]:
+        out = g.empty((1,), torch.int32)
+        g.call("tlh_argmax", g.dev(x), x.size, out)
+        assert int(g.host(out)[0]) == O.argmax(x)
+
+
+def test_argmax_rows(g):
+    x = O.normal((64, 2048), 36)
+    x[3, [10, 20]] = 99.0
+    out = g.empty((64,), torch.int32)
+    g.call("tlh_argmax_rows", g.dev(x), 64, 2048, out)
+    got = g.host(out)
+    for r in range(64):
+        assert got[r] == O.argmax(x[r])
+
+
+def test_gradient_norm_single_and_multi(g):
+    # KAT 169 (test_metal_runtime.cpp:595-615) + GPT-sized multi-tensor
+    first, second = np.array([3, 4, 0], np.float32), np.array([12], np.float32)
+    s = g.zeros((1,))
+    g.call("tlh_accumulate_gradient_squared_norm", g.dev(first), 3, s)
+    g.call("tlh_accumulate_gradient_squared_norm", g.dev(second), 1, s)
+    assert abs(g.host(s)[0] - 169.0) < 1e-5
+    sizes = [384 * 384, 384, 1536 * 384, 1536, 2048 * 384, 7, 1]
+    grads = [g.dev(O.normal((n,), 40 + i)) for i, n in enumerate(sizes)]
+    ptrs = torch.tensor([t.data_ptr() for t in grads], dtype=torch.int64, device="cuda")
+    dsz = torch.tensor(sizes, dtype=torch.int64, device="cuda")
+    partials = g.empty((1024,))
+    out = g.empty((1,))
+    g.call("tlh_gradient_squared_norm_multi", ptrs, dsz, len(sizes), partials, out)
+    expect = sum(float((g.host(t).astype(np.float64) ** 2).sum()) for t in grads)
+    assert abs(g.host(out)[0] - expect) / expect < 1e-5
+
+
+def test_column_sum(g):
+    x = O.normal((6144, 384), 50)
+    old = O.normal((384,), 51)
+    out = g.dev(old)
+    g.call("tlh_column_sum", g.dev(x), 6144, 384, out, 1.0)
+    assert_close(g.host(out), O.sum_to_shape(x, [384]) + old, rtol=1e-4, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# row ops
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(6144, 2048), (36864, 192), (2, 3), (100, 2500), (7, 1)])
+def test_softmax(g, rows, cols):
+    x = O.normal((rows, cols), 52, 0, 3)
+    out = g.empty((rows, cols))
+    g.call("tlh_softmax", g.dev(x), out, rows, cols)
+    assert_close(g.host(out), O.softmax(x))
+
+
+def test_softmax_stability_kat(g):
+    # test_metal_runtime.cpp:432-472 rank-4 with +-1000 rows
+    x = np.array([1, 2, 3, 3, 2, 1, 1000, 1001, 1002, -1000, -1000, -1000], np.float32)
+    out = g.empty((4, 3))
+    g.call("tlh_softmax", g.dev(x.reshape(4, 3)), out, 4, 3)
+    assert_close(g.host(out), O.softmax(x.reshape(4, 3)))
+
+
+@pytest.mark.parametrize("rows,cols", [(36864, 192), (50, 77)])
+def test_softmax_backward(g, rows, cols):
+    y = O.softmax(O.normal((rows, cols), 53, 0, 2))
+    gr = O.normal((rows, cols), 54)
+    out = g.empty((rows, cols))
+    g.call("tlh_softmax_backward", g.dev(gr), g.dev(y), out, rows, cols)
+    assert_close(g.host(out), O.softmax_backward(gr, y), rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,vocab", [(6144, 2048), (4, 3), (33, 1000)])
+def test_cross_entropy(g, rows, vocab):
+    logits = O.normal((rows, vocab), 55, 0, 2)
+    t = O.uniform_u32((rows,), 56, vocab)
+    t[0] = vocab  # invalid target -> +INF row
+    loss = g.empty((rows,))
+    g.call("tlh_cross_entropy_rows", g.dev(logits), g.dev(t), loss, rows, vocab)
+    assert_close(g.host(loss), O.cross_entropy(logits, t)[:, 0])
+    grad = g.empty((rows, vocab))
+    g.call("tlh_cross_entropy_rows_backward", g.dev(logits), g.dev(t), grad, rows, vocab, None)
+    assert_close(g.host(grad), O.cross_entropy_backward(logits, t), rtol=1e-4, atol=1e-6)
+    scale = 1.0 / rows
+    loss2, grad2 = g.empty((rows,)), g.empty((rows, vocab))
+    g.call("tlh_cross_entropy_rows_fused", g.dev(logits), g.dev(t), loss2, grad2, rows, vocab,
+           scale)
+    assert_close(g.host(loss2), O.cross_entropy(logits, t)[:, 0])
+    expect = O.cross_entropy_backward(logits, t) * np.float32(scale)
+    assert_close(g.host(grad2), expect, rtol=1e-4, atol=1e-8)
+
+
+@pytest.mark.parametrize("rows,cols", [(6144, 384), (8192, 1024), (2, 2), (10, 300)])
+@pytest.mark.parametrize("with_gain", [False, True])
+def test_rms_norm(g, rows, cols, with_gain):
+    x = O.normal((rows, cols), 57)
+    if rows == 2:
+        x = np.array([[3, 4], [0, 0]], np.float32)  # KAT: zero row -> rms = 1e-3
+    gain = O.normal((cols,), 58, 1, 0.02) if with_gain else None
+    eps = 1e-5 if with_gain else 1e-6
+    y, r = g.empty((rows, cols)), g.empty((rows,))
+    g.call("tlh_rms_norm", g.dev(x), g.dev(gain) if with_gain else None, y, r, rows, cols, eps)
+    assert_close(g.host(y), O.rms_norm(x, gain, eps))
+    assert_close(g.host(r), O.rms(x, eps)[:, 0])
+    r2 = g.empty((rows,))
+    g.call("tlh_rms", g.dev(x), r2, rows, cols, eps)
+    assert_close(g.host(r2), O.rms(x, eps)[:, 0])
+
+
+@pytest.mark.parametrize("rows,cols", [(6144, 384), (9, 300)])
+@pytest.mark.parametrize("with_gain", [False, True])
+def test_rms_norm_backward(g, rows, cols, with_gain):
+    x, gr = O.normal((rows, cols), 59), O.normal((rows, cols), 60)
+    gain = O.normal((cols,), 61, 1, 0.02) if with_gain else None
+    old = O.normal((rows, cols), 62)
+    dx = g.dev(old)
+    dgain = g.empty((cols,)) if with_gain else None
+    g.call("tlh_rms_norm_backward", g.dev(gr), g.dev(x), g.dev(gain) if with_gain else None,
+           dx, dgain, rows, cols, 1e-6, 1.0)
+    edx, edgain = O.rms_norm_backward(gr, x, gain, 1e-6)
+    assert_close(g.host(dx), edx + old, rtol=1e-4, atol=1e-5)
+    if with_gain:
+        assert_close(g.host(dgain), edgain, rtol=1e-4, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# embedding
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,dim,n", [(2048, 384, 6144), (4, 3, 4), (192, 1023, 50)])
+def test_embedding_lookup_bit_exact(g, rows, dim, n):
+    w = O.normal((rows, dim), 63)
+    ids = O.uniform_u32((n,), 64, rows)
+    out = g.empty((n, dim))
+    g.call("tlh_embedding_lookup", g.dev(w), rows, dim, g.dev(ids), n, out)
+    np.testing.assert_array_equal(g.host(out), O.embedding_lookup(w, ids))
+
+
+def test_embedding_add_positions(g):
+    B, T, D, V = 32, 192, 384, 2048
+    tok, pos = O.normal((V, D), 65), O.normal((T, D), 66)
+    ids = O.uniform_u32((B, T), 67, V)
+    out = g.empty((B, T, D))
+    g.call("tlh_embedding_add_positions", g.dev(tok), g.dev(pos), g.dev(ids), B, T, D, out)
+    expect = O.embedding_lookup(tok, ids) + pos[None, :, :]
+    np.testing.assert_array_equal(g.host(out), expect)
+
+
+def test_scatter_add_rows(g):
+    # KAT (test_metal_runtime.cpp:571-593) then the GPT shape
+    base = np.arange(100, 112, dtype=np.float32).reshape(4, 3)
+    values = np.array([1, 2, 3, 4, 5, 6, 10, 20, 30, 7, 8, 9], np.float32).reshape(4, 3)
+    ids = np.array([2, 0, 2, 1], np.uint32)
+    dst = g.dev(base)
+    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), 4, 3, dst)
+    np.testing.assert_allclose(g.host(dst), O.scatter_add_rows(base, ids, values), atol=1e-4)
+    V, D, n = 2048, 384, 6144
+    values = O.normal((n, D), 68)
+    ids = O.uniform_u32((n,), 69, V)
+    dst = g.zeros((V, D))
+    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), n, D, dst)
+    assert_close(g.host(dst), O.scatter_add_rows(np.zeros((V, D), np.float32), ids, values),
+                 rtol=1e-4, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# optimiser
+# ---------------------------------------------------------------------------
+def test_clip_kat(g):
+    s = g.dev(np.array([169.0], np.float32))
+    x = g.dev(np.array([3, 4, 0], np.float32))
+    g.call("tlh_clip_gradient", x, s, 1.0, x, 3)
+    assert_close(g.host(x), [3 / 13, 4 / 13, 0])
+
+
+def test_adamw_two_steps(g):
+    n = 100003
+    p, gr = O.normal((n,), 70), O.normal((n,), 71)
+    m1 = np.zeros(n, np.float32); m2 = np.zeros(n, np.float32)
+    lr, b1, b2, wd, eps = 3e-4, 0.9, 0.95, 0.1, 1e-8
+    decay = float(np.float32(1) - np.float32(lr) * np.float32(wd))
+    sc = [g.dev(np.array([v], np.float32)) for v in (b1, b2, decay, lr)]
+    dp, dg, dm1, dm2 = g.dev(p), g.dev(gr), g.dev(m1), g.dev(m2)
+    ep, em1, em2 = p, m1, m2
+    for step in (1, 2):
+        g.call("tlh_adamw", dp, dg, dp, dm1, dm2, *sc, eps, step, n)
+        ep, em1, em2 = O.adamw(ep, gr, em1, em2, b1, b2, decay, lr, eps, step)
+        assert_close(g.host(dp), ep, rtol=1e-4, atol=1e-6)
+        assert_close(g.host(dm1), em1)
+        assert_close(g.host(dm2), em2, rtol=1e-4, atol=1e-9)
+
+
+def test_adamw_multi_matches_per_tensor(g):
+    sizes = [384 * 384, 384, 4097, 1, 2048 * 384]
+    lr, b1, b2, wd, eps, max_norm = 3e-4, 0.9, 0.95, 0.1, 1e-8, 1.0
+    decay = float(np.float32(1) - np.float32(lr) * np.float32(wd))
+    ps = [O.normal((n,), 80 + i) for i, n in enumerate(sizes)]
+    gs = [O.normal((n,), 90 + i) for i, n in enumerate(sizes)]
+    m1s = [O.normal((n,), 100 + i, 0, 0.01) for i, n in enumerate(sizes)]
+    m2s = [np.abs(O.normal((n,), 110 + i, 0, 0.01)) for i, n in enumerate(sizes)]
+    steps = [3, 3, 1, 7, 2]
+    sq = sum(float((x.astype(np.float64) ** 2).sum()) for x in gs)
+    dev = [[g.dev(x) for x in arr] for arr in (ps, gs, m1s, m2s)]
+    tabs = [torch.tensor([t.data_ptr() for t in arr], dtype=torch.int64, device="cuda")
+            for arr in dev]
+    dsz = torch.tensor(sizes, dtype=torch.int64, device="cuda")
+    dst = torch.tensor(steps, dtype=torch.int32, device="cuda")
+    sc = [g.dev(np.array([v], np.float32)) for v in (b1, b2, decay, lr)]
+    dsq = g.dev(np.array([sq], np.float32))
+    g.call("tlh_adamw_multi", *tabs, dsz, dst, len(sizes), *sc, eps, dsq, max_norm)
+    for i in range(len(sizes)):
+        gc = O.clip_gradient(gs[i], np.float32(sq), max_norm)
+        ep, em1, em2 = O.adamw(ps[i], gc, m1s[i], m2s[i], b1, b2, decay, lr, eps, steps[i])
+        assert_close(g.host(dev[0][i]), ep, rtol=1e-4, atol=1e-6, what=f"param {i}")
+        assert_close(g.host(dev[2][i]), em1, what=f"m1 {i}")
+        assert_close(g.host(dev[3][i]), em2, rtol=1e-4, atol=1e-9, what=f"m2 {i}")
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,H,T,causal", [(4, 6, 192, True), (2, 3, 100, True),
+                                          (2, 2, 130, False), (1, 1, 1, True)])
+@pytest.mark.parametrize("merged", [False, True])
+def test_attention_forward_backward(g, B, H, T, causal, merged):
+    D = 64
+    q, k, v = (O.normal((B, H, T, D), s, 0, 0.125) for s in (120, 121, 122))
+    dout_h = O.normal((B, H, T, D), 123)
+    o_ref, probs = O.attention_forward(q, k, v, causal)
+    dq_r, dk_r, dv_r = O.attention_backward(q, k, v, probs, dout_h)
+
+    def to_layout(x):  # [B,H,T,D] -> merged [B,T,H*D]
+        return np.ascontiguousarray(x.transpose(0, 2, 1, 3).reshape(B, T, H * D)) if merged else x
+
+    dq_, dk_, dv_ = g.dev(q), g.dev(k), g.dev(v)
+    o = g.empty((B * H * T * D,))
+    lse = g.empty((B * H * T,))
+    g.call("tlh_attention_forward", dq_, dk_, dv_, o, lse, B, H, T, D, 0.125, int(causal),
+           int(merged))
+    assert_rel(g.host(o).reshape(to_layout(o_ref).shape), to_layout(o_ref), 1e-3, "O")
+    delta = g.empty((B * H * T,))
+    dq, dk, dv = (g.empty((B * H * T * D,)) for _ in range(3))
+    g.call("tlh_attention_backward", dq_, dk_, dv_, o, g.dev(to_layout(dout_h)), lse, delta, dq, dk,
+           dv, B, H, T, D, 0.125, int(causal), int(merged), int(merged))
+    for got, ref, name in ((dq, dq_r, "dQ"), (dk, dk_r, "dK"), (dv, dv_r, "dV")):
+        assert_rel(g.host(got).reshape(to_layout(ref).shape), to_layout(ref), 1e-3, name)
