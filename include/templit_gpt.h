@@ -1,0 +1,104 @@
+/*
+ * templit_gpt.h -- C-ABI of libtemplit_gpt.so: the GPT training-step
+ * program that drives libtemplit_hip.so.
+ *
+ * This is the program layer above the runtime surface. In the reference
+ * the same work is done by passes::Compiled over nn::GPT
+ * (include/passes/compile.h:37-304, include/nn/GPT.h:17-69) and the
+ * training loop of src/train.cpp:120-187: forward(), backward(root_grad),
+ * step(max_norm) with AdamW. Here the step is a fixed sequence of fused
+ * gfx950 kernels on one HIP stream with lifetime-planned device buffers,
+ * recordable as one hipGraph and replayed every step.
+ *
+ * Model (nn::GPT): token + position embedding, `layers` pre-RMSNorm decoder
+ * blocks (causal multi-head attention with Q/K/V/O linears, GELU FFN of
+ * width `ffn`), final RMSNorm, vocabulary projection; loss = per-row
+ * cross-entropy. Parameters are fp32 and live in one device allocation in
+ * this canonical order (tlg_param_info gives each tensor's offset):
+ *   tok [V,D], pos [T,D], per layer: wq [D,D], bq [D], wk, bk, wv, bv,
+ *   wo, bo, w1 [D,F], b1 [F], w2 [F,D], b2 [D]; then wp [D,V], bp [V].
+ * Weights are stored [in, out] row-major as nn::Layer does (y = x.W + b).
+ *
+ * Conventions as in templit_hip.h: int return = hipError_t (0 = success),
+ * device pointers unless host_*, asynchronous on the program's stream.
+ */
+#ifndef TEMPLIT_GPT_H
+#define TEMPLIT_GPT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tlg_config {
+  uint32_t vocab, seq, dim, heads, layers, batch, ffn;
+} tlg_config;
+
+/* Allocates parameters, gradients, AdamW state and every activation /
+ * scratch buffer of one step (nothing is allocated per step). head dim must
+ * be 64. `stream` = hipStream_t used for all work. */
+int tlg_create(const tlg_config *cfg, void *stream, void **program);
+int tlg_destroy(void *program);
+
+/* Parameter table: count, and per tensor its element count and device
+ * pointer (params / grads / AdamW moments share one layout). */
+int tlg_param_count(void *program, uint32_t *count);
+int tlg_param_info(void *program, uint32_t index, uint64_t *size, float **param,
+                   float **grad, float **m1, float **m2);
+/* Total elements of the flat canonical (unpadded) parameter vector. */
+int tlg_total_params(void *program, uint64_t *total);
+
+/* Host <-> device copies of the flat canonical parameter vector. Synchronous. */
+int tlg_set_params(void *program, const float *host_params);
+int tlg_get_params(void *program, float *host_params);
+int tlg_get_grads(void *program, float *host_grads);
+int tlg_get_moments(void *program, float *host_m1, float *host_m2);
+/* AdamW per-tensor step counters (AdamW::step_, AdamW.h:42,78) and the
+ * optimiser scalars {beta1, beta2, decay, lr} as the device holds them. */
+int tlg_get_steps(void *program, uint32_t *host_steps);
+int tlg_get_scalars(void *program, float *host_scalars4);
+/* Device-side init: weights ~ N(0, std) (SplitMix64 + Box-Muller per
+ * element), biases 0, moments 0, step counters 0. */
+int tlg_init_params(void *program, uint64_t seed, float std);
+
+/* AdamW hyper-parameters (Optimiser::AdamW::Shared, AdamW.h:15-39): lr and
+ * decay = 1 - lr*weight_decay live in device scalars, so changing them does
+ * not invalidate a captured step. */
+int tlg_set_optimizer(void *program, float lr, float beta1, float beta2, float eps,
+                      float weight_decay);
+int tlg_set_lr(void *program, float lr);
+
+/* Device buffers the step reads its batch from (uint32 [B*T] each) and
+ * writes per-row losses to (float [B*T]); stable for the program's life. */
+int tlg_io(void *program, uint32_t **tokens, uint32_t **targets, float **losses,
+           float **logits);
+
+/* One training step on the batch in the io buffers: forward, per-row loss,
+ * backward with uniform root gradient `root_grad` (src/train.cpp:109-113),
+ * global squared gradient norm, clip to max_norm (if > 0) and AdamW.
+ * update = 0 runs forward + backward only (gradients left in grad buffers). */
+int tlg_train_step(void *program, float root_grad, float max_norm, int update);
+/* Forward only: logits [B*T, V] into the io logits buffer. */
+int tlg_forward(void *program);
+/* Squared gradient norm of the last step (host read, synchronous). */
+int tlg_last_squared_norm(void *program, float *host_value);
+
+/* One eager training step with HIP events recorded on the program's stream
+ * around every GEMM launch and every attention launch: returns the summed
+ * GEMM time (ms), the GEMMs' algorithmic flops (2*M*N*K each), the number
+ * of GEMM launches, the summed attention time and the whole step's time. */
+int tlg_profile_step(void *program, float root_grad, float max_norm, float *host_gemm_ms,
+                     double *host_gemm_flops, uint32_t *host_gemm_launches,
+                     float *host_attention_ms, float *host_step_ms);
+
+/* Records tlg_train_step(root_grad, max_norm, 1) as a hipGraph; replays it. */
+int tlg_capture_train_step(void *program, float root_grad, float max_norm);
+int tlg_replay(void *program);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

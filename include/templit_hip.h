@@ -72,6 +72,18 @@ int tlh_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
  * (runtime.cpp:1018-1027). Kernel fills, safe inside captured graphs. */
 int tlh_fill_f32(float *dst, float value, size_t n, void *stream);
 int tlh_fill_u32(uint32_t *dst, uint32_t value, size_t n, void *stream);
+/* counters[i] += delta on the stream: AdamW's per-parameter ++step_
+ * (include/optimiser/AdamW.h:78) as a kernel, so a captured training step
+ * advances the step count on every replay. */
+int tlh_increment_u32(uint32_t *counters, size_t n, uint32_t delta, void *stream);
+/* Synthetic data on the device: element i of dst is the i-th value of a
+ * SplitMix64 stream seeded with `seed` (normal: Box-Muller over pairs;
+ * uniform: next() % bound). Used for random-init weights and benchmark
+ * batches; the reference draws these on the host (include/nn/layer.h:15-30). */
+int tlh_fill_normal(float *dst, size_t n, uint64_t seed, float mean, float std,
+                    void *stream);
+int tlh_fill_uniform_u32(uint32_t *dst, size_t n, uint64_t seed, uint32_t bound,
+                         void *stream);
 /* Storage::compare (storage.h:52-59): byte equality. `scratch` is one device
  * int. Synchronous. */
 int tlh_compare(const void *a, const void *b, size_t bytes, int *host_equal,

@@ -23,6 +23,39 @@ __global__ void fill_u32_kernel(uint32_t *dst, uint32_t value, size_t n) {
     dst[i] = value;
 }
 
+__global__ void increment_u32_kernel(uint32_t *c, size_t n, uint32_t delta) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += size_t(gridDim.x) * blockDim.x)
+    c[i] += delta;
+}
+
+// SplitMix64 output number i+1 of the stream seeded with `seed`.
+__device__ inline uint64_t splitmix_at(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_kernel(float *dst, size_t n, uint64_t seed, float mean, float std) {
+  const size_t pairs = (n + 1) / 2;
+  for (size_t p = size_t(blockIdx.x) * blockDim.x + threadIdx.x; p < pairs;
+       p += size_t(gridDim.x) * blockDim.x) {
+    const double u1 = double((splitmix_at(seed, 2 * p) >> 11) + 1) * (1.0 / 9007199254740992.0);
+    const double u2 = double((splitmix_at(seed, 2 * p + 1) >> 11) + 1) * (1.0 / 9007199254740992.0);
+    const double r = sqrt(-2.0 * log(u1));
+    const double t = 6.283185307179586 * u2;
+    dst[2 * p] = float(mean + std * r * cos(t));
+    if (2 * p + 1 < n) dst[2 * p + 1] = float(mean + std * r * sin(t));
+  }
+}
+
+__global__ void fill_uniform_u32_kernel(uint32_t *dst, size_t n, uint64_t seed, uint32_t bound) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += size_t(gridDim.x) * blockDim.x)
+    dst[i] = uint32_t(splitmix_at(seed, i) % bound);
+}
+
 __global__ void compare_kernel(const uint32_t *a, const uint32_t *b, size_t n,
                                int *differs) {
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -114,6 +147,29 @@ TLH_API int tlh_memcpy_d2d(void *dst, const void *src, size_t bytes, void *strea
 TLH_API int tlh_fill_u32(uint32_t *dst, uint32_t value, size_t n, void *stream) {
   if (n == 0) return 0;
   fill_u32_kernel<<<stride_grid(n, 256), 256, 0, as_stream(stream)>>>(dst, value, n);
+  return launch_status();
+}
+
+TLH_API int tlh_increment_u32(uint32_t *counters, size_t n, uint32_t delta, void *stream) {
+  if (n == 0) return 0;
+  increment_u32_kernel<<<stride_grid(n, 256), 256, 0, as_stream(stream)>>>(counters, n, delta);
+  return launch_status();
+}
+
+TLH_API int tlh_fill_normal(float *dst, size_t n, uint64_t seed, float mean, float std,
+                            void *stream) {
+  if (n == 0) return 0;
+  fill_normal_kernel<<<stride_grid((n + 1) / 2, 256), 256, 0, as_stream(stream)>>>(dst, n, seed,
+                                                                                  mean, std);
+  return launch_status();
+}
+
+TLH_API int tlh_fill_uniform_u32(uint32_t *dst, size_t n, uint64_t seed, uint32_t bound,
+                                 void *stream) {
+  if (n == 0) return 0;
+  if (bound == 0) return int(hipErrorInvalidValue);
+  fill_uniform_u32_kernel<<<stride_grid(n, 256), 256, 0, as_stream(stream)>>>(dst, n, seed,
+                                                                              bound);
   return launch_status();
 }
 

@@ -1,0 +1,630 @@
+// GPT training-step program over the C-ABI of libtemplit_hip.so.
+//
+// The reference runs this model through passes::Compiled
+// (include/passes/compile.h:148-258): ~1,269 runtime calls per step, every
+// op writing a fresh temporary, the backward re-evaluating shared gradient
+// expressions, explicit transposes before every matmul derivative, and 52
+// clip + 52 AdamW launches. Here the same mathematics is a fixed list of
+// ~170 fused launches on one stream:
+//   forward   embed(+pos) | per layer: RMSNorm, Q/K/V GEMMs storing the
+//             [B,H,T,64] head layout, fused causal attention, O GEMM
+//             (+bias +residual), RMSNorm, W1 GEMM (+bias, GELU), W2 GEMM
+//             (+bias +residual) | RMSNorm, vocab GEMM, fused CE fwd+bwd
+//   backward  transposed-operand GEMMs (no materialised transposes),
+//             GELU' fused into the dG GEMM epilogue, fused RMSNorm',
+//             attention backward, split-K weight gradients
+//   step      one multi-tensor squared norm, one multi-tensor clip+AdamW.
+// Every buffer is allocated once in tlg_create (lifetime planned by hand:
+// activations kept for the backward, one shared scratch set), so the whole
+// step can be captured as a hipGraph and replayed.
+#include "templit_gpt.h"
+#include "templit_hip.h"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace {
+
+struct Tensor {
+  float *ptr = nullptr;
+  size_t size = 0;
+};
+
+constexpr uint32_t kHeadDim = 64;
+constexpr float kRmsEps = 1e-6f; // src/my_metal/runtime.cpp:1044
+constexpr size_t kAlign = 64;    // floats: every tensor starts 256-byte aligned
+
+struct Program {
+  tlg_config cfg{};
+  void *stream = nullptr;
+  size_t R = 0; // rows = B*T
+
+  // parameters / gradients / moments: one allocation each, same offsets
+  std::vector<size_t> offset, size;
+  size_t padded_total = 0, total = 0;
+  float *params = nullptr, *grads = nullptr, *m1 = nullptr, *m2 = nullptr;
+  // device tables for the multi-tensor kernels
+  void *tab_params = nullptr, *tab_grads = nullptr, *tab_m1 = nullptr, *tab_m2 = nullptr;
+  uint64_t *tab_sizes = nullptr;
+  uint32_t *steps = nullptr;
+  // optimiser scalars (device): beta1, beta2, decay, lr
+  float *scalars = nullptr;
+  float eps = 1e-8f, weight_decay = 0.01f, lr = 1e-3f;
+  float *norm_partials = nullptr, *sqnorm = nullptr;
+
+  // io
+  uint32_t *tokens = nullptr, *targets = nullptr;
+  float *losses = nullptr, *logits = nullptr, *dlogits = nullptr;
+
+  // activations (per layer) and scratch
+  std::vector<float *> x;        // L+1 residual-stream inputs [R,D]
+  std::vector<float *> n1, q, k, v, o, lse, x_mid, n2, u, g;
+  float *nf = nullptr;
+  float *dx = nullptr, *tmp = nullptr, *dgf = nullptr, *dq = nullptr, *dk = nullptr,
+        *dv = nullptr, *delta = nullptr, *workspace = nullptr;
+  size_t workspace_elems = 0;
+
+  std::vector<void *> allocations;
+  void *graph = nullptr;
+
+  // profiling (eager steps only): event pairs around GEMM / attention launches
+  bool profiling = false;
+  std::vector<void *> events;
+  size_t next_event = 0;
+  std::vector<std::pair<void *, void *>> gemm_spans, attn_spans;
+  double gemm_flops = 0.0;
+
+  float *P(uint32_t i) const { return params + offset[i]; }
+  float *G(uint32_t i) const { return grads + offset[i]; }
+};
+
+int alloc(Program &p, void **ptr, size_t bytes) {
+  const int st = tlh_malloc(ptr, bytes < 256 ? 256 : bytes);
+  if (st == 0) p.allocations.push_back(*ptr);
+  return st;
+}
+
+int allocf(Program &p, float **ptr, size_t elems) {
+  return alloc(p, reinterpret_cast<void **>(ptr), elems * sizeof(float));
+}
+
+// Parameter shapes in canonical order.
+void layout(Program &p) {
+  const size_t V = p.cfg.vocab, T = p.cfg.seq, D = p.cfg.dim, F = p.cfg.ffn;
+  std::vector<size_t> sizes = {V * D, T * D};
+  for (uint32_t l = 0; l < p.cfg.layers; ++l) {
+    const size_t layer[12] = {D * D, D, D * D, D, D * D, D, D * D, D, D * F, F, F * D, D};
+    sizes.insert(sizes.end(), layer, layer + 12);
+  }
+  sizes.push_back(D * V);
+  sizes.push_back(V);
+  size_t off = 0;
+  p.total = 0;
+  for (size_t s : sizes) {
+    p.offset.push_back(off);
+    p.size.push_back(s);
+    off += (s + kAlign - 1) / kAlign * kAlign;
+    p.total += s;
+  }
+  p.padded_total = off;
+}
+
+tlh_gemm_desc desc(const float *a, const float *b, float *c, int m, int n, int k, bool ta,
+                   bool tb) {
+  tlh_gemm_desc d;
+  std::memset(&d, 0, sizeof(d));
+  d.a = a;
+  d.b = b;
+  d.c = c;
+  d.m = m;
+  d.n = n;
+  d.k = k;
+  d.trans_a = ta;
+  d.trans_b = tb;
+  d.lda = ta ? m : k;
+  d.ldb = tb ? k : n;
+  d.ldc = n;
+  return d;
+}
+
+#define TRY(x)                                                                                 \
+  do {                                                                                         \
+    const int st_ = (x);                                                                       \
+    if (st_) return st_;                                                                       \
+  } while (0)
+
+void *event(Program &p) {
+  if (p.next_event == p.events.size()) {
+    void *e = nullptr;
+    if (tlh_event_create(&e)) return nullptr;
+    p.events.push_back(e);
+  }
+  return p.events[p.next_event++];
+}
+
+// Records an event pair around `launch` when profiling.
+template <typename F>
+int timed(Program &p, std::vector<std::pair<void *, void *>> &spans, F &&launch) {
+  if (!p.profiling) return launch();
+  void *a = event(p), *b = event(p);
+  if (!a || !b) return 1;
+  TRY(tlh_event_record(a, p.stream));
+  TRY(launch());
+  TRY(tlh_event_record(b, p.stream));
+  spans.emplace_back(a, b);
+  return 0;
+}
+
+int gemm(Program &p, tlh_gemm_desc d) {
+  if (d.trans_a) d.workspace = p.workspace; // tall-K weight gradients may split K
+  if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k;
+  return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, p.stream); });
+}
+
+int forward(Program &p) {
+  const tlg_config &c = p.cfg;
+  const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
+  TRY(tlh_embedding_add_positions(p.P(0), p.P(1), p.tokens, c.batch, c.seq, c.dim, p.x[0],
+                                  p.stream));
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    const uint32_t w = 2 + 12 * l;
+    TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, p.R, c.dim, kRmsEps, p.stream));
+    float *qkv[3] = {p.q[l], p.k[l], p.v[l]};
+    for (int j = 0; j < 3; ++j) {
+      tlh_gemm_desc d = desc(p.n1[l], p.P(w + 2 * j), qkv[j], R, D, D, false, false);
+      d.bias = p.P(w + 2 * j + 1);
+      d.remap_t = int(c.seq);
+      d.remap_h = int(c.heads);
+      d.remap_d = int(kHeadDim);
+      TRY(gemm(p, d));
+    }
+    TRY(timed(p, p.attn_spans, [&] {
+      return tlh_attention_forward(p.q[l], p.k[l], p.v[l], p.o[l], p.lse[l], c.batch, c.heads,
+                                   c.seq, kHeadDim, 1.0f / std::sqrt(float(kHeadDim)), 1, 1,
+                                   p.stream);
+    }));
+    {
+      tlh_gemm_desc d = desc(p.o[l], p.P(w + 6), p.x_mid[l], R, D, D, false, false);
+      d.bias = p.P(w + 7);
+      d.residual = p.x[l];
+      TRY(gemm(p, d));
+    }
+    TRY(tlh_rms_norm(p.x_mid[l], nullptr, p.n2[l], nullptr, p.R, c.dim, kRmsEps, p.stream));
+    {
+      tlh_gemm_desc d = desc(p.n2[l], p.P(w + 8), p.g[l], R, F, D, false, false);
+      d.bias = p.P(w + 9);
+      d.epilogue = TLH_EPI_GELU;
+      d.aux = p.u[l];
+      TRY(gemm(p, d));
+    }
+    {
+      tlh_gemm_desc d = desc(p.g[l], p.P(w + 10), p.x[l + 1], R, D, F, false, false);
+      d.bias = p.P(w + 11);
+      d.residual = p.x_mid[l];
+      TRY(gemm(p, d));
+    }
+  }
+  TRY(tlh_rms_norm(p.x[c.layers], nullptr, p.nf, nullptr, p.R, c.dim, kRmsEps, p.stream));
+  const uint32_t last = 2 + 12 * c.layers;
+  tlh_gemm_desc d = desc(p.nf, p.P(last), p.logits, R, V, D, false, false);
+  d.bias = p.P(last + 1);
+  return gemm(p, d);
+}
+
+int backward(Program &p) {
+  const tlg_config &c = p.cfg;
+  const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
+  const uint32_t last = 2 + 12 * c.layers;
+  // vocab projection
+  TRY(gemm(p, desc(p.nf, p.dlogits, p.G(last), D, V, R, true, false)));
+  TRY(tlh_column_sum(p.dlogits, p.R, c.vocab, p.G(last + 1), 0.0f, p.stream));
+  TRY(gemm(p, desc(p.dlogits, p.P(last), p.tmp, R, D, V, false, true)));
+  TRY(tlh_rms_norm_backward(p.tmp, p.x[c.layers], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
+                            0.0f, p.stream));
+  for (int l = int(c.layers) - 1; l >= 0; --l) {
+    const uint32_t w = 2 + 12 * uint32_t(l);
+    // FFN: x[l+1] = x_mid + W2.GELU(W1.n2 + b1) + b2
+    TRY(gemm(p, desc(p.g[l], p.dx, p.G(w + 10), F, D, R, true, false)));
+    TRY(tlh_column_sum(p.dx, p.R, c.dim, p.G(w + 11), 0.0f, p.stream));
+    {
+      tlh_gemm_desc d = desc(p.dx, p.P(w + 10), p.dgf, R, F, D, false, true);
+      d.epilogue = TLH_EPI_GELU_BWD;
+      d.aux = p.u[l];
+      TRY(gemm(p, d));
+    }
+    TRY(gemm(p, desc(p.n2[l], p.dgf, p.G(w + 8), D, F, R, true, false)));
+    TRY(tlh_column_sum(p.dgf, p.R, c.ffn, p.G(w + 9), 0.0f, p.stream));
+    TRY(gemm(p, desc(p.dgf, p.P(w + 8), p.tmp, R, D, F, false, true)));
+    TRY(tlh_rms_norm_backward(p.tmp, p.x_mid[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
+                              1.0f, p.stream));
+    // attention: x_mid = x + Wo.attn(n1) + bo
+    TRY(gemm(p, desc(p.o[l], p.dx, p.G(w + 6), D, D, R, true, false)));
+    TRY(tlh_column_sum(p.dx, p.R, c.dim, p.G(w + 7), 0.0f, p.stream));
+    TRY(gemm(p, desc(p.dx, p.P(w + 6), p.tmp, R, D, D, false, true)));
+    TRY(timed(p, p.attn_spans, [&] {
+      return tlh_attention_backward(p.q[l], p.k[l], p.v[l], p.o[l], p.tmp, p.lse[l], p.delta,
+                                    p.dq, p.dk, p.dv, c.batch, c.heads, c.seq, kHeadDim,
+                                    1.0f / std::sqrt(float(kHeadDim)), 1, 1, 1, p.stream);
+    }));
+    float *dqkv[3] = {p.dq, p.dk, p.dv};
+    for (int j = 0; j < 3; ++j) {
+      TRY(gemm(p, desc(p.n1[l], dqkv[j], p.G(w + 2 * j), D, D, R, true, false)));
+      TRY(tlh_column_sum(dqkv[j], p.R, c.dim, p.G(w + 2 * j + 1), 0.0f, p.stream));
+    }
+    for (int j = 0; j < 3; ++j) {
+      tlh_gemm_desc d = desc(dqkv[j], p.P(w + 2 * j), p.tmp, R, D, D, false, true);
+      d.beta = j == 0 ? 0.0f : 1.0f;
+      TRY(gemm(p, d));
+    }
+    TRY(tlh_rms_norm_backward(p.tmp, p.x[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps, 1.0f,
+                              p.stream));
+  }
+  // embeddings: scatter_index for tokens (zero + scatter_add_rows), positions
+  // as a column sum over the batch of the [B, T*D] view.
+  TRY(tlh_fill_f32(p.G(0), 0.0f, p.size[0], p.stream));
+  TRY(tlh_scatter_add_rows(p.dx, p.tokens, p.R, c.dim, p.G(0), p.stream));
+  return tlh_column_sum(p.dx, c.batch, c.seq * c.dim, p.G(1), 0.0f, p.stream);
+}
+
+int optimizer_step(Program &p, float max_norm) {
+  const uint32_t count = uint32_t(p.size.size());
+  TRY(tlh_gradient_squared_norm_multi(reinterpret_cast<const float *const *>(p.tab_grads),
+                                      p.tab_sizes, count, p.norm_partials, p.sqnorm, p.stream));
+  TRY(tlh_increment_u32(p.steps, count, 1, p.stream));
+  return tlh_adamw_multi(reinterpret_cast<float *const *>(p.tab_params),
+                         reinterpret_cast<const float *const *>(p.tab_grads),
+                         reinterpret_cast<float *const *>(p.tab_m1),
+                         reinterpret_cast<float *const *>(p.tab_m2), p.tab_sizes, p.steps, count,
+                         p.scalars, p.scalars + 1, p.scalars + 2, p.scalars + 3, p.eps,
+                         max_norm > 0.0f ? p.sqnorm : nullptr, max_norm, p.stream);
+}
+
+int train_step(Program &p, float root_grad, float max_norm, int update) {
+  TRY(forward(p));
+  TRY(tlh_cross_entropy_rows_fused(p.logits, p.targets, p.losses, p.dlogits, p.R, p.cfg.vocab,
+                                   root_grad, p.stream));
+  TRY(backward(p));
+  if (!update) {
+    const uint32_t count = uint32_t(p.size.size());
+    return tlh_gradient_squared_norm_multi(reinterpret_cast<const float *const *>(p.tab_grads),
+                                           p.tab_sizes, count, p.norm_partials, p.sqnorm,
+                                           p.stream);
+  }
+  return optimizer_step(p, max_norm);
+}
+
+int write_scalars(Program &p, float beta1, float beta2) {
+  const float decay = 1.0f - p.lr * p.weight_decay; // AdamW.h:28-29, fp32 on the host
+  const float host[4] = {beta1, beta2, decay, p.lr};
+  TRY(tlh_memcpy_h2d(p.scalars, host, sizeof(host), p.stream));
+  return tlh_stream_synchronize(p.stream);
+}
+
+int create(Program &p) {
+  const tlg_config &c = p.cfg;
+  const size_t R = p.R, D = c.dim, F = c.ffn, V = c.vocab, B = c.batch, H = c.heads,
+               T = c.seq, L = c.layers;
+  layout(p);
+  TRY(allocf(p, &p.params, p.padded_total));
+  TRY(allocf(p, &p.grads, p.padded_total));
+  TRY(allocf(p, &p.m1, p.padded_total));
+  TRY(allocf(p, &p.m2, p.padded_total));
+  const size_t count = p.size.size();
+  TRY(alloc(p, &p.tab_params, count * sizeof(void *)));
+  TRY(alloc(p, &p.tab_grads, count * sizeof(void *)));
+  TRY(alloc(p, &p.tab_m1, count * sizeof(void *)));
+  TRY(alloc(p, &p.tab_m2, count * sizeof(void *)));
+  TRY(alloc(p, reinterpret_cast<void **>(&p.tab_sizes), count * sizeof(uint64_t)));
+  TRY(alloc(p, reinterpret_cast<void **>(&p.steps), count * sizeof(uint32_t)));
+  TRY(allocf(p, &p.scalars, 4));
+  TRY(allocf(p, &p.norm_partials, TLH_NORM_PARTIALS));
+  TRY(allocf(p, &p.sqnorm, 1));
+  {
+    std::vector<void *> tp(count), tg(count), t1(count), t2(count);
+    std::vector<uint64_t> sz(count);
+    for (size_t i = 0; i < count; ++i) {
+      tp[i] = p.params + p.offset[i];
+      tg[i] = p.grads + p.offset[i];
+      t1[i] = p.m1 + p.offset[i];
+      t2[i] = p.m2 + p.offset[i];
+      sz[i] = p.size[i];
+    }
+    TRY(tlh_memcpy_h2d(p.tab_params, tp.data(), count * sizeof(void *), p.stream));
+    TRY(tlh_memcpy_h2d(p.tab_grads, tg.data(), count * sizeof(void *), p.stream));
+    TRY(tlh_memcpy_h2d(p.tab_m1, t1.data(), count * sizeof(void *), p.stream));
+    TRY(tlh_memcpy_h2d(p.tab_m2, t2.data(), count * sizeof(void *), p.stream));
+    TRY(tlh_memcpy_h2d(p.tab_sizes, sz.data(), count * sizeof(uint64_t), p.stream));
+    TRY(tlh_stream_synchronize(p.stream));
+  }
+  TRY(tlh_fill_u32(p.steps, 0, count, p.stream));
+  TRY(tlh_fill_f32(p.params, 0.0f, p.padded_total, p.stream));
+  TRY(tlh_fill_f32(p.grads, 0.0f, p.padded_total, p.stream));
+  TRY(tlh_fill_f32(p.m1, 0.0f, p.padded_total, p.stream));
+  TRY(tlh_fill_f32(p.m2, 0.0f, p.padded_total, p.stream));
+
+  TRY(alloc(p, reinterpret_cast<void **>(&p.tokens), R * sizeof(uint32_t)));
+  TRY(alloc(p, reinterpret_cast<void **>(&p.targets), R * sizeof(uint32_t)));
+  TRY(tlh_fill_u32(p.tokens, 0, R, p.stream));
+  TRY(tlh_fill_u32(p.targets, 0, R, p.stream));
+  TRY(allocf(p, &p.losses, R));
+  TRY(allocf(p, &p.logits, R * V));
+  TRY(allocf(p, &p.dlogits, R * V));
+  p.x.resize(L + 1);
+  for (auto &b : p.x) TRY(allocf(p, &b, R * D));
+  for (auto *vec : {&p.n1, &p.q, &p.k, &p.v, &p.o, &p.x_mid, &p.n2}) {
+    vec->resize(L);
+    for (auto &b : *vec) TRY(allocf(p, &b, R * D));
+  }
+  p.lse.resize(L);
+  for (auto &b : p.lse) TRY(allocf(p, &b, B * H * T));
+  p.u.resize(L);
+  p.g.resize(L);
+  for (size_t l = 0; l < L; ++l) {
+    TRY(allocf(p, &p.u[l], R * F));
+    TRY(allocf(p, &p.g[l], R * F));
+  }
+  TRY(allocf(p, &p.nf, R * D));
+  TRY(allocf(p, &p.dx, R * D));
+  TRY(allocf(p, &p.tmp, R * D));
+  TRY(allocf(p, &p.dgf, R * F));
+  TRY(allocf(p, &p.dq, R * D));
+  TRY(allocf(p, &p.dk, R * D));
+  TRY(allocf(p, &p.dv, R * D));
+  TRY(allocf(p, &p.delta, B * H * T));
+  // split-K workspace: the largest any weight-gradient GEMM asks for
+  size_t ws = 0;
+  const int shapes[4][2] = {{int(D), int(V)}, {int(F), int(D)}, {int(D), int(F)},
+                            {int(D), int(D)}};
+  for (auto &s : shapes) {
+    tlh_gemm_desc d = desc(nullptr, nullptr, nullptr, s[0], s[1], int(R), true, false);
+    size_t e = 0;
+    tlh_gemm_workspace_size(&d, &e);
+    if (e > ws) ws = e;
+  }
+  p.workspace_elems = ws;
+  if (ws) TRY(allocf(p, &p.workspace, ws));
+  p.lr = 1e-3f;
+  TRY(write_scalars(p, 0.9f, 0.999f));
+  return tlh_stream_synchronize(p.stream);
+}
+
+void release(Program &p) {
+  if (p.graph) tlh_graph_destroy(p.graph);
+  for (void *e : p.events) tlh_event_destroy(e);
+  p.events.clear();
+  for (void *a : p.allocations) tlh_free(a);
+  p.allocations.clear();
+}
+
+int copy_params(Program &p, float *dev_base, const float *host, bool to_device) {
+  // flat canonical host vector <-> padded device layout
+  size_t flat = 0;
+  for (size_t i = 0; i < p.size.size(); ++i) {
+    const size_t bytes = p.size[i] * sizeof(float);
+    if (to_device) {
+      TRY(tlh_memcpy_h2d(dev_base + p.offset[i], host + flat, bytes, p.stream));
+    } else {
+      TRY(tlh_memcpy_d2h(const_cast<float *>(host) + flat, dev_base + p.offset[i], bytes,
+                         p.stream));
+    }
+    flat += p.size[i];
+  }
+  return tlh_stream_synchronize(p.stream);
+}
+
+bool is_bias(const Program &p, uint32_t i) {
+  if (i < 2) return false;
+  const uint32_t last = 2 + 12 * p.cfg.layers;
+  if (i == last) return false;
+  if (i == last + 1) return true;
+  return ((i - 2) % 12) % 2 == 1;
+}
+
+} // namespace
+
+extern "C" {
+
+int tlg_create(const tlg_config *cfg, void *stream, void **program) {
+  *program = nullptr;
+  if (!cfg || cfg->heads == 0 || cfg->dim != cfg->heads * kHeadDim || cfg->vocab == 0 ||
+      cfg->seq == 0 || cfg->batch == 0 || cfg->layers == 0 || cfg->ffn == 0)
+    return 1; // hipErrorInvalidValue
+  Program *p = new (std::nothrow) Program();
+  if (!p) return 2; // hipErrorOutOfMemory
+  p->cfg = *cfg;
+  p->stream = stream;
+  p->R = size_t(cfg->batch) * cfg->seq;
+  const int st = create(*p);
+  if (st) {
+    release(*p);
+    delete p;
+    return st;
+  }
+  *program = p;
+  return 0;
+}
+
+int tlg_destroy(void *program) {
+  if (!program) return 0;
+  Program *p = static_cast<Program *>(program);
+  tlh_stream_synchronize(p->stream);
+  release(*p);
+  delete p;
+  return 0;
+}
+
+int tlg_param_count(void *program, uint32_t *count) {
+  *count = uint32_t(static_cast<Program *>(program)->size.size());
+  return 0;
+}
+
+int tlg_param_info(void *program, uint32_t index, uint64_t *size, float **param, float **grad,
+                   float **m1, float **m2) {
+  Program *p = static_cast<Program *>(program);
+  if (index >= p->size.size()) return 1;
+  if (size) *size = p->size[index];
+  if (param) *param = p->params + p->offset[index];
+  if (grad) *grad = p->grads + p->offset[index];
+  if (m1) *m1 = p->m1 + p->offset[index];
+  if (m2) *m2 = p->m2 + p->offset[index];
+  return 0;
+}
+
+int tlg_total_params(void *program, uint64_t *total) {
+  *total = static_cast<Program *>(program)->total;
+  return 0;
+}
+
+int tlg_set_params(void *program, const float *host_params) {
+  Program *p = static_cast<Program *>(program);
+  return copy_params(*p, p->params, host_params, true);
+}
+
+int tlg_get_params(void *program, float *host_params) {
+  Program *p = static_cast<Program *>(program);
+  return copy_params(*p, p->params, host_params, false);
+}
+
+int tlg_get_grads(void *program, float *host_grads) {
+  Program *p = static_cast<Program *>(program);
+  return copy_params(*p, p->grads, host_grads, false);
+}
+
+int tlg_get_moments(void *program, float *host_m1, float *host_m2) {
+  Program *p = static_cast<Program *>(program);
+  TRY(copy_params(*p, p->m1, host_m1, false));
+  return copy_params(*p, p->m2, host_m2, false);
+}
+
+int tlg_get_steps(void *program, uint32_t *host_steps) {
+  Program *p = static_cast<Program *>(program);
+  TRY(tlh_memcpy_d2h(host_steps, p->steps, p->size.size() * sizeof(uint32_t), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_get_scalars(void *program, float *host_scalars4) {
+  Program *p = static_cast<Program *>(program);
+  TRY(tlh_memcpy_d2h(host_scalars4, p->scalars, 4 * sizeof(float), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_init_params(void *program, uint64_t seed, float std) {
+  Program *p = static_cast<Program *>(program);
+  for (uint32_t i = 0; i < p->size.size(); ++i) {
+    float *dst = p->params + p->offset[i];
+    if (is_bias(*p, i)) {
+      TRY(tlh_fill_f32(dst, 0.0f, p->size[i], p->stream));
+    } else {
+      TRY(tlh_fill_normal(dst, p->size[i], seed + 7919ull * i, 0.0f, std, p->stream));
+    }
+  }
+  TRY(tlh_fill_f32(p->m1, 0.0f, p->padded_total, p->stream));
+  TRY(tlh_fill_f32(p->m2, 0.0f, p->padded_total, p->stream));
+  TRY(tlh_fill_u32(p->steps, 0, p->size.size(), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_set_optimizer(void *program, float lr, float beta1, float beta2, float eps,
+                      float weight_decay) {
+  Program *p = static_cast<Program *>(program);
+  p->lr = lr;
+  p->eps = eps;
+  p->weight_decay = weight_decay;
+  return write_scalars(*p, beta1, beta2);
+}
+
+int tlg_set_lr(void *program, float lr) {
+  Program *p = static_cast<Program *>(program);
+  p->lr = lr;
+  const float host[2] = {1.0f - lr * p->weight_decay, lr};
+  TRY(tlh_memcpy_h2d(p->scalars + 2, host, sizeof(host), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_io(void *program, uint32_t **tokens, uint32_t **targets, float **losses,
+           float **logits) {
+  Program *p = static_cast<Program *>(program);
+  if (tokens) *tokens = p->tokens;
+  if (targets) *targets = p->targets;
+  if (losses) *losses = p->losses;
+  if (logits) *logits = p->logits;
+  return 0;
+}
+
+int tlg_train_step(void *program, float root_grad, float max_norm, int update) {
+  return train_step(*static_cast<Program *>(program), root_grad, max_norm, update);
+}
+
+int tlg_forward(void *program) { return forward(*static_cast<Program *>(program)); }
+
+int tlg_last_squared_norm(void *program, float *host_value) {
+  Program *p = static_cast<Program *>(program);
+  TRY(tlh_memcpy_d2h(host_value, p->sqnorm, sizeof(float), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_profile_step(void *program, float root_grad, float max_norm, float *host_gemm_ms,
+                     double *host_gemm_flops, uint32_t *host_gemm_launches,
+                     float *host_attention_ms, float *host_step_ms) {
+  Program *p = static_cast<Program *>(program);
+  TRY(tlh_stream_synchronize(p->stream));
+  p->profiling = true;
+  p->next_event = 0;
+  p->gemm_spans.clear();
+  p->attn_spans.clear();
+  p->gemm_flops = 0.0;
+  void *start = event(*p), *end = event(*p);
+  int st = (start && end) ? tlh_event_record(start, p->stream) : 1;
+  if (!st) st = train_step(*p, root_grad, max_norm, 1);
+  if (!st) st = tlh_event_record(end, p->stream);
+  p->profiling = false;
+  TRY(st);
+  TRY(tlh_stream_synchronize(p->stream));
+  float total = 0.0f, ms = 0.0f;
+  for (auto &s : p->gemm_spans) {
+    TRY(tlh_event_elapsed_ms(s.first, s.second, &ms));
+    total += ms;
+  }
+  float attn = 0.0f;
+  for (auto &s : p->attn_spans) {
+    TRY(tlh_event_elapsed_ms(s.first, s.second, &ms));
+    attn += ms;
+  }
+  TRY(tlh_event_elapsed_ms(start, end, &ms));
+  *host_gemm_ms = total;
+  *host_gemm_flops = p->gemm_flops;
+  *host_gemm_launches = uint32_t(p->gemm_spans.size());
+  *host_attention_ms = attn;
+  *host_step_ms = ms;
+  return 0;
+}
+
+int tlg_capture_train_step(void *program, float root_grad, float max_norm) {
+  Program *p = static_cast<Program *>(program);
+  if (p->graph) {
+    tlh_graph_destroy(p->graph);
+    p->graph = nullptr;
+  }
+  TRY(tlh_stream_synchronize(p->stream));
+  TRY(tlh_graph_begin_capture(p->stream));
+  const int st = train_step(*p, root_grad, max_norm, 1);
+  void *exec = nullptr;
+  const int st2 = tlh_graph_end_capture(p->stream, &exec);
+  if (st) {
+    if (exec) tlh_graph_destroy(exec);
+    return st;
+  }
+  if (st2) return st2;
+  p->graph = exec;
+  return 0;
+}
+
+int tlg_replay(void *program) {
+  Program *p = static_cast<Program *>(program);
+  if (!p->graph) return 1;
+  return tlh_graph_launch(p->graph, p->stream);
+}
+
+} // extern "C"

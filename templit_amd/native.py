@@ -55,6 +55,9 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_memcpy_d2d": [P, P, c_size_t, P],
     "tlh_fill_f32": [P, c_float, c_size_t, P],
     "tlh_fill_u32": [P, c_uint32, c_size_t, P],
+    "tlh_increment_u32": [P, c_size_t, c_uint32, P],
+    "tlh_fill_normal": [P, c_size_t, c_uint64, c_float, c_float, P],
+    "tlh_fill_uniform_u32": [P, c_size_t, c_uint64, c_uint32, P],
     "tlh_compare": [P, P, c_size_t, POINTER(c_int), P, P],
     "tlh_event_create": [POINTER(c_void_p)],
     "tlh_event_record": [P, P],
@@ -164,3 +167,205 @@ def addr(x) -> int:
     if x is None:
         return 0
     return ctypes.addressof(x)
+
+
+# ---------------------------------------------------------------------------
+# libtemplit_gpt.so (include/templit_gpt.h)
+# ---------------------------------------------------------------------------
+class GptConfig(ctypes.Structure):
+    """Mirror of struct tlg_config."""
+
+    _fields_ = [("vocab", c_uint32), ("seq", c_uint32), ("dim", c_uint32),
+                ("heads", c_uint32), ("layers", c_uint32), ("batch", c_uint32),
+                ("ffn", c_uint32)]
+
+
+FP = POINTER(c_void_p)
+GPT_SIGNATURES: dict[str, list] = {
+    "tlg_create": [POINTER(GptConfig), P, POINTER(c_void_p)],
+    "tlg_destroy": [P],
+    "tlg_param_count": [P, POINTER(c_uint32)],
+    "tlg_param_info": [P, c_uint32, POINTER(c_uint64), FP, FP, FP, FP],
+    "tlg_total_params": [P, POINTER(c_uint64)],
+    "tlg_set_params": [P, P],
+    "tlg_get_params": [P, P],
+    "tlg_get_grads": [P, P],
+    "tlg_get_moments": [P, P, P],
+    "tlg_get_steps": [P, P],
+    "tlg_get_scalars": [P, P],
+    "tlg_init_params": [P, c_uint64, c_float],
+    "tlg_set_optimizer": [P, c_float, c_float, c_float, c_float, c_float],
+    "tlg_set_lr": [P, c_float],
+    "tlg_io": [P, FP, FP, FP, FP],
+    "tlg_train_step": [P, c_float, c_float, c_int],
+    "tlg_forward": [P],
+    "tlg_last_squared_norm": [P, POINTER(c_float)],
+    "tlg_profile_step": [P, c_float, c_float, POINTER(c_float), POINTER(ctypes.c_double),
+                         POINTER(c_uint32), POINTER(c_float), POINTER(c_float)],
+    "tlg_capture_train_step": [P, c_float, c_float],
+    "tlg_replay": [P],
+}
+
+_GPT: ctypes.CDLL | None = None
+
+
+def load_gpt() -> ctypes.CDLL:
+    """Loads libtemplit_gpt.so (and through it libtemplit_hip.so)."""
+    global _GPT
+    if _GPT is not None:
+        return _GPT
+    load_hip()
+    if not GPT_LIB.exists():
+        raise NativeError(
+            f"{GPT_LIB} is missing: build it with `python -m templit_amd.build`")
+    lib = ctypes.CDLL(str(GPT_LIB))
+    for name, argtypes in GPT_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = c_int
+    _GPT = lib
+    return lib
+
+
+class GptProgram:
+    """Thin owner of a tlg program handle (all work happens in native code)."""
+
+    def __init__(self, vocab, seq, dim, heads, layers, batch, ffn=None, stream=None):
+        import numpy as np  # local: numpy is only needed by this helper
+
+        self._np = np
+        self.lib = load_gpt()
+        hip = load_hip()
+        check(hip.tlh_init(0), "tlh_init")
+        self.cfg = GptConfig(vocab, seq, dim, heads, layers, batch, ffn or 4 * dim)
+        self.own_stream = stream is None
+        if stream is None:
+            s = c_void_p()
+            check(hip.tlh_stream_create(ctypes.byref(s)), "tlh_stream_create")
+            stream = s.value
+        self.stream = stream
+        h = c_void_p()
+        check(self.lib.tlg_create(ctypes.byref(self.cfg), stream, ctypes.byref(h)), "tlg_create")
+        self.handle = h.value
+        tot = c_uint64()
+        check(self.lib.tlg_total_params(self.handle, ctypes.byref(tot)), "tlg_total_params")
+        self.total = tot.value
+        ptrs = [c_void_p() for _ in range(4)]
+        check(self.lib.tlg_io(self.handle, *[ctypes.byref(x) for x in ptrs]), "tlg_io")
+        self.tokens_ptr, self.targets_ptr, self.losses_ptr, self.logits_ptr = (
+            x.value for x in ptrs)
+        self.rows = batch * seq
+
+    def close(self):
+        if self.handle:
+            self.lib.tlg_destroy(self.handle)
+            self.handle = None
+        if self.own_stream and self.stream:
+            load_hip().tlh_stream_destroy(self.stream)
+            self.stream = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- host <-> device ----------------------------------------------------
+    def set_params(self, flat):
+        flat = self._np.ascontiguousarray(flat, dtype=self._np.float32)
+        assert flat.size == self.total
+        check(self.lib.tlg_set_params(self.handle, flat.ctypes.data), "tlg_set_params")
+
+    def get_params(self):
+        out = self._np.empty(self.total, self._np.float32)
+        check(self.lib.tlg_get_params(self.handle, out.ctypes.data), "tlg_get_params")
+        return out
+
+    def get_grads(self):
+        out = self._np.empty(self.total, self._np.float32)
+        check(self.lib.tlg_get_grads(self.handle, out.ctypes.data), "tlg_get_grads")
+        return out
+
+    def get_moments(self):
+        a = self._np.empty(self.total, self._np.float32)
+        b = self._np.empty(self.total, self._np.float32)
+        check(self.lib.tlg_get_moments(self.handle, a.ctypes.data, b.ctypes.data),
+              "tlg_get_moments")
+        return a, b
+
+    def set_batch(self, tokens, targets):
+        hip = load_hip()
+        for arr, ptr in ((tokens, self.tokens_ptr), (targets, self.targets_ptr)):
+            a = self._np.ascontiguousarray(arr, dtype=self._np.uint32)
+            assert a.size == self.rows
+            check(hip.tlh_memcpy_h2d(ptr, a.ctypes.data, a.nbytes, self.stream), "h2d")
+            check(hip.tlh_stream_synchronize(self.stream), "sync")
+
+    def random_batch(self, seed):
+        hip = load_hip()
+        check(hip.tlh_fill_uniform_u32(self.tokens_ptr, self.rows, seed, self.cfg.vocab,
+                                       self.stream), "tokens")
+        check(hip.tlh_fill_uniform_u32(self.targets_ptr, self.rows, seed + 1, self.cfg.vocab,
+                                       self.stream), "targets")
+
+    def losses(self):
+        hip = load_hip()
+        out = self._np.empty(self.rows, self._np.float32)
+        check(hip.tlh_memcpy_d2h(out.ctypes.data, self.losses_ptr, out.nbytes, self.stream), "d2h")
+        check(hip.tlh_stream_synchronize(self.stream), "sync")
+        return out
+
+    def logits(self):
+        hip = load_hip()
+        out = self._np.empty((self.rows, self.cfg.vocab), self._np.float32)
+        check(hip.tlh_memcpy_d2h(out.ctypes.data, self.logits_ptr, out.nbytes, self.stream), "d2h")
+        check(hip.tlh_stream_synchronize(self.stream), "sync")
+        return out
+
+    def steps(self):
+        n = c_uint32()
+        check(self.lib.tlg_param_count(self.handle, ctypes.byref(n)), "count")
+        out = self._np.empty(n.value, self._np.uint32)
+        check(self.lib.tlg_get_steps(self.handle, out.ctypes.data), "steps")
+        return out
+
+    def scalars(self):
+        out = self._np.empty(4, self._np.float32)
+        check(self.lib.tlg_get_scalars(self.handle, out.ctypes.data), "scalars")
+        return out
+
+    def squared_norm(self):
+        v = c_float()
+        check(self.lib.tlg_last_squared_norm(self.handle, ctypes.byref(v)), "norm")
+        return v.value
+
+    # -- steps ---------------------------------------------------------------
+    def init_params(self, seed, std):
+        check(self.lib.tlg_init_params(self.handle, seed, std), "tlg_init_params")
+
+    def set_optimizer(self, lr, beta1, beta2, eps, weight_decay):
+        check(self.lib.tlg_set_optimizer(self.handle, lr, beta1, beta2, eps, weight_decay),
+              "tlg_set_optimizer")
+
+    def train_step(self, root_grad, max_norm, update=True):
+        check(self.lib.tlg_train_step(self.handle, root_grad, max_norm, int(update)), "train_step")
+
+    def forward(self):
+        check(self.lib.tlg_forward(self.handle), "forward")
+
+    def capture(self, root_grad, max_norm):
+        check(self.lib.tlg_capture_train_step(self.handle, root_grad, max_norm), "capture")
+
+    def profile_step(self, root_grad, max_norm):
+        gm, fl, n, am, sm = c_float(), ctypes.c_double(), c_uint32(), c_float(), c_float()
+        check(self.lib.tlg_profile_step(self.handle, root_grad, max_norm, ctypes.byref(gm),
+                                        ctypes.byref(fl), ctypes.byref(n), ctypes.byref(am),
+                                        ctypes.byref(sm)), "profile_step")
+        return dict(gemm_ms=gm.value, gemm_flops=fl.value, gemm_launches=n.value,
+                    attention_ms=am.value, step_ms=sm.value)
+
+    def replay(self):
+        check(self.lib.tlg_replay(self.handle), "replay")
+
+    def synchronize(self):
+        check(load_hip().tlh_stream_synchronize(self.stream), "sync")

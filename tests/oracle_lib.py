@@ -372,6 +372,15 @@ def gpt_param_sizes(cfg: GptConfig) -> list[int]:
     return [int(lib().orc_gpt_param_size(ctypes.byref(cfg), i)) for i in range(n)]
 
 
+def gpt_key_bias_indices(cfg: GptConfig) -> list[int]:
+    """Indices of the K-projection biases. Their gradient is exactly zero:
+    q.(k_j + b) = q.k_j + q.b shifts every score of a query row by the same
+    constant and softmax is shift invariant, so both the oracle and the GPU
+    hold only rounding noise there (and AdamW's first step turns that noise
+    into +-lr)."""
+    return [2 + 12 * l + 3 for l in range(cfg.layers)]
+
+
 def gpt_train_step(cfg: GptConfig, params, m, v, step, tokens, targets, root_grad, lr, beta1,
                    beta2, eps, weight_decay, max_norm):
     params, m, v = _f32(params).copy(), _f32(m).copy(), _f32(v).copy()

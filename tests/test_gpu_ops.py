@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle_lib as O
-from gpu_util import Gpu, assert_close, assert_rel, u32
+from gpu_util import Gpu, assert_close, assert_rel, rel_err, u32
 from templit_amd.native import EPI_GELU, EPI_GELU_BWD, GemmDesc
 
 pytestmark = pytest.mark.gpu
@@ -526,5 +526,10 @@ def test_attention_forward_backward(g, B, H, T, causal, merged):
     dq, dk, dv = (g.empty((B * H * T * D,)) for _ in range(3))
     g.call("tlh_attention_backward", dq_, dk_, dv_, o, g.dev(to_layout(dout_h)), lse, delta, dq, dk,
            dv, B, H, T, D, 0.125, int(causal), int(merged), int(merged))
+    # A gradient that is exactly zero (dQ, dK at T=1: softmax over one key)
+    # is compared against the scale of the whole backward output.
+    scale = max(float(np.abs(r).max()) for r in (dq_r, dk_r, dv_r))
     for got, ref, name in ((dq, dq_r, "dQ"), (dk, dk_r, "dK"), (dv, dv_r, "dV")):
-        assert_rel(g.host(got).reshape(to_layout(ref).shape), to_layout(ref), 1e-3, name)
+        err = rel_err(g.host(got).reshape(to_layout(ref).shape), to_layout(ref),
+                      floor=1e-3 * scale)
+        assert err <= 1e-3, f"{name}: relative error {err:.3e}"
