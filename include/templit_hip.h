@@ -196,6 +196,11 @@ typedef struct tlh_gemm_desc {
   /* if remap_h > 0: element (m = b*remap_t + t, n = h*remap_d + d) is stored
    * at ((b*remap_h + h)*remap_t + t)*remap_d + d */
   int32_t remap_t, remap_h, remap_d;
+  /* if non-NULL: bias_grad[n] = beta*bias_grad[n] + sum_k op(B)[k][n]. For a
+   * weight gradient C = X^T.dY this is the bias gradient (the reference's
+   * sum_to_shape of dY to [1,N], runtime.cpp:661-739), computed from the dY
+   * tiles the GEMM already stages in LDS. Not with remap_* or batching. */
+  float *bias_grad;
 } tlh_gemm_desc;
 
 int tlh_gemm(const tlh_gemm_desc *desc, void *stream);

@@ -19,6 +19,9 @@ struct GemmDesc {
   const float *bias = nullptr;     // [N] row vector, optional
   const float *residual = nullptr; // [M,N] added after bias, same indexing as C
   float *aux = nullptr;            // GELU pre-activation (written or read), same indexing as C
+  // Bias gradient of a weight gradient: bias_grad[n] = beta*bias_grad[n] +
+  // sum_k op(B)[k][n] (the column sums of dY when C = X^T.dY).
+  float *bias_grad = nullptr;
   int M = 0, N = 0, K = 0;
   int lda = 0, ldb = 0, ldc = 0;
   int trans_a = 0, trans_b = 0;
@@ -35,9 +38,10 @@ struct GemmDesc {
   uint32_t batch_stride_a[4] = {0, 0, 0, 0};
   uint32_t batch_stride_b[4] = {0, 0, 0, 0};
   uint32_t batch_stride_c[4] = {0, 0, 0, 0};
-  // Split-K (batch == 1 only): partial products go to `workspace`
-  // ([splits, M, N]) and a reduction kernel applies the epilogue.
-  int splits = 1;
+  // Split-K (batch == 1 only, chosen by gemm_launch when a workspace is
+  // given): partial products go to `workspace` ([splits, M, N] then
+  // [splits, N] bias-gradient partials) and a reduction kernel applies the
+  // epilogue in a fixed order.
   float *workspace = nullptr;
 };
 
@@ -45,7 +49,7 @@ struct GemmDesc {
 int gemm_launch(const GemmDesc &d, void *stream);
 
 // Number of fp32 elements of split-K workspace gemm_launch wants for `d`
-// under its own tile/split choice (0 = no split). `d.splits` is ignored.
+// under its own tile/split choice (0 = no split).
 size_t gemm_workspace_elems(const GemmDesc &d);
 
 // Chooses the split count gemm_launch would use for `d` (1 = none).

@@ -34,6 +34,7 @@ struct GemmParams {
   const float *residual;
   float *aux;
   float *workspace;
+  float *bias_grad;
   int M, N, K;
   int lda, ldb, ldc;
   float beta;
@@ -251,6 +252,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     }
   };
 
+  // Bias gradient: the blocks of the first tile row also sum the op(B)
+  // tiles they stage (threads = BN columns x 256/BN k groups).
+  const bool do_bias = p.bias_grad != nullptr && tm == 0;
+  constexpr int BGROUPS = 256 / BN;
+  const int bcol = tid % BN, bgrp = tid / BN;
+  float bsum = 0.f;
+
   const int nk = (k_end > k_begin) ? (k_end - k_begin + BK - 1) / BK : 0;
   if (nk > 0) {
     load_tile(k_begin);
@@ -260,8 +268,29 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int cur = kt & 1;
       if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * BK);
       compute_tile(cur);
+      if (do_bias) {
+        const float *bs = smem + cur * (A_TILE + B_TILE) + A_TILE;
+#pragma unroll
+        for (int kk = bgrp; kk < BK; kk += BGROUPS)
+          bsum += TB ? bs[bcol * B_LD + kk] : bs[kk * B_LD + bcol];
+      }
       if (kt + 1 < nk) store_tile(cur ^ 1);
       __syncthreads();
+    }
+  }
+  if (do_bias) { // every thread is past the loop's last barrier: smem is free
+    smem[tid] = bsum;
+    __syncthreads();
+    const int n = n0 + tid;
+    if (tid < BN && n < p.N) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < BGROUPS; ++g) t += smem[g * BN + tid];
+      if (p.splits > 1) {
+        p.workspace[size_t(p.splits) * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
+      } else {
+        p.bias_grad[n] = p.beta != 0.0f ? t + p.beta * p.bias_grad[n] : t;
+      }
     }
   }
 
@@ -288,20 +317,27 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 
 // Sums the split-K partials and applies the epilogue; deterministic order.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
-  const size_t total = size_t(p.M) * p.N;
-  const size_t plane = total;
+  const size_t plane = size_t(p.M) * p.N;
+  const size_t total = plane + (p.bias_grad ? size_t(p.N) : 0);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += size_t(gridDim.x) * blockDim.x) {
-    float s = 0.f;
-    for (int z = 0; z < p.splits; ++z) s += p.workspace[z * plane + i];
-    const int m = int(i / p.N);
-    const int n = int(i - size_t(m) * p.N);
-    epilogue_store(p, p.C, m, n, s);
+    if (i < plane) {
+      float s = 0.f;
+      for (int z = 0; z < p.splits; ++z) s += p.workspace[z * plane + i];
+      const int m = int(i / p.N);
+      const int n = int(i - size_t(m) * p.N);
+      epilogue_store(p, p.C, m, n, s);
+    } else {
+      const size_t n = i - plane;
+      float s = 0.f;
+      for (int z = 0; z < p.splits; ++z) s += p.workspace[size_t(p.splits) * plane + z * size_t(p.N) + n];
+      p.bias_grad[n] = p.beta != 0.0f ? s + p.beta * p.bias_grad[n] : s;
+    }
   }
 }
 
-struct TileCfg {
-  int bm, bn;
+struct Plan {
+  int bm, bn, splits;
 };
 
 template <int BM, int BN, int WM, int WN>
@@ -327,12 +363,29 @@ inline size_t tiles_for(const GemmDesc &d, int bm, int bn) {
   return size_t((d.M + bm - 1) / bm) * size_t((d.N + bn - 1) / bn);
 }
 
-TileCfg choose_tile(const GemmDesc &d) {
+constexpr int kTargetBlocks = 256; // one block per CU at least
+constexpr int kMinSplitK = 128;    // K elements per split-K chunk, at least
+
+// Largest tile that still gives every CU a block; otherwise (tall-K weight
+// gradients) the largest tile whose split-K count reaches 256 blocks with
+// K chunks of >= 128.
+Plan make_plan(const GemmDesc &d, bool allow_split) {
+  static const int cfgs[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
   const size_t batch = size_t(std::max(1, d.batch));
-  if (tiles_for(d, 128, 128) * batch >= 240) return {128, 128};
-  if (tiles_for(d, 128, 64) * batch >= 240) return {128, 64};
-  if (tiles_for(d, 64, 128) * batch >= 240) return {64, 128};
-  return {64, 64};
+  for (const auto &c : cfgs)
+    if (tiles_for(d, c[0], c[1]) * batch >= kTargetBlocks) return {c[0], c[1], 1};
+  if (allow_split && batch == 1 && d.batch_ndim == 0 && d.K >= 4 * kMinSplitK) {
+    for (const auto &c : cfgs) {
+      const size_t tiles = tiles_for(d, c[0], c[1]);
+      int splits = int((kTargetBlocks + tiles - 1) / tiles);
+      splits = std::min(std::min(splits, d.K / kMinSplitK), 64);
+      if (splits >= 2 && tiles * splits >= kTargetBlocks) return {c[0], c[1], splits};
+    }
+    const size_t tiles = tiles_for(d, 64, 64);
+    const int splits = std::max(1, std::min(d.K / kMinSplitK, 64));
+    return {64, 64, tiles < kTargetBlocks ? splits : 1};
+  }
+  return {64, 64, 1};
 }
 
 bool vec_ok(const GemmDesc &d) {
@@ -350,34 +403,24 @@ bool vec_ok(const GemmDesc &d) {
 
 } // namespace
 
-int gemm_choose_splits(const GemmDesc &d) {
-  if (d.batch > 1 || d.batch_ndim > 0) return 1;
-  const TileCfg t = choose_tile(d);
-  const size_t tiles = tiles_for(d, t.bm, t.bn);
-  if (tiles >= 200 || d.K < 512) return 1;
-  // Aim for ~2 waves of blocks over 256 CUs with K chunks of >= 128.
-  int splits = int((512 + tiles - 1) / tiles);
-  splits = std::min(splits, d.K / 128);
-  splits = std::max(1, std::min(splits, 64));
-  return splits;
-}
+int gemm_choose_splits(const GemmDesc &d) { return make_plan(d, true).splits; }
 
 size_t gemm_workspace_elems(const GemmDesc &d) {
   const int s = gemm_choose_splits(d);
-  return s > 1 ? size_t(s) * d.M * d.N : 0;
+  // C partials [s, M, N] followed by bias-gradient partials [s, N]
+  return s > 1 ? size_t(s) * (size_t(d.M) * d.N + d.N) : 0;
 }
 
 int gemm_launch(const GemmDesc &d, void *stream) {
   if (d.M <= 0 || d.N <= 0) return 0;
-  if (d.K <= 0) {
-    // Empty reduction: C = epilogue(0); handled by the split-K reducer path
-    // with zero splits worth of partials.
-  }
+  if (d.bias_grad && (d.batch > 1 || d.batch_ndim > 0 || d.remap_h > 0))
+    return int(hipErrorInvalidValue);
   hipStream_t s = as_stream(stream);
   GemmParams p{};
   p.A = d.A; p.B = d.B; p.C = d.C;
   p.bias = d.bias; p.residual = d.residual; p.aux = d.aux;
   p.workspace = d.workspace;
+  p.bias_grad = d.bias_grad;
   p.M = d.M; p.N = d.N; p.K = d.K;
   p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc;
   p.beta = d.beta;
@@ -390,30 +433,29 @@ int gemm_launch(const GemmDesc &d, void *stream) {
     p.bsb[i] = d.batch_stride_b[i];
     p.bsc[i] = d.batch_stride_c[i];
   }
-  const TileCfg t = choose_tile(d);
-  p.tiles_n = (d.N + t.bn - 1) / t.bn;
-  const int tiles_m = (d.M + t.bm - 1) / t.bm;
-  p.splits = (d.splits > 1 && d.workspace) ? d.splits : 1;
-  if (p.splits > 1 && (d.batch > 1 || d.batch_ndim > 0)) return int(hipErrorInvalidValue);
+  const Plan plan = make_plan(d, d.workspace != nullptr);
+  p.tiles_n = (d.N + plan.bn - 1) / plan.bn;
+  const int tiles_m = (d.M + plan.bm - 1) / plan.bm;
+  p.splits = plan.splits;
   p.k_chunk = p.splits > 1 ? ((d.K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : d.K;
-  if (p.splits > 1) p.splits = (d.K + p.k_chunk - 1) / p.k_chunk;
-  if (d.K <= 0) {
-    // Nothing to accumulate: run the reducer over zero partials.
+  if (p.splits > 1) p.splits = (d.K + p.k_chunk - 1) / p.k_chunk; // <= plan.splits
+  const size_t reduce_elems = size_t(d.M) * d.N + (d.bias_grad ? d.N : 0);
+  if (d.K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
-    gemm_splitk_reduce<<<stride_grid(size_t(d.M) * d.N, 256), 256, 0, s>>>(p);
+    gemm_splitk_reduce<<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     return launch_status();
   }
   const int z = p.splits > 1 ? p.splits : std::max(1, d.batch);
   dim3 grid(unsigned(tiles_m * p.tiles_n), 1, unsigned(z));
   const bool ta = d.trans_a != 0, tb = d.trans_b != 0, vec = vec_ok(d);
-  if (t.bm == 128 && t.bn == 128) launch_cfg<128, 128, 64, 64>(p, ta, tb, vec, grid, s);
-  else if (t.bm == 128 && t.bn == 64) launch_cfg<128, 64, 64, 32>(p, ta, tb, vec, grid, s);
-  else if (t.bm == 64 && t.bn == 128) launch_cfg<64, 128, 32, 64>(p, ta, tb, vec, grid, s);
+  if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64>(p, ta, tb, vec, grid, s);
+  else if (plan.bm == 128 && plan.bn == 64) launch_cfg<128, 64, 64, 32>(p, ta, tb, vec, grid, s);
+  else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64>(p, ta, tb, vec, grid, s);
   else launch_cfg<64, 64, 32, 32>(p, ta, tb, vec, grid, s);
   int st = launch_status();
   if (st) return st;
   if (p.splits > 1) {
-    gemm_splitk_reduce<<<stride_grid(size_t(d.M) * d.N, 256), 256, 0, s>>>(p);
+    gemm_splitk_reduce<<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     st = launch_status();
   }
   return st;
@@ -438,6 +480,7 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
   d.beta = c.beta;
   d.epilogue = c.epilogue;
   d.remap_t = c.remap_t; d.remap_h = c.remap_h; d.remap_d = c.remap_d;
+  d.bias_grad = c.bias_grad;
   return d;
 }
 } // namespace
@@ -451,7 +494,6 @@ TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
   if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 || d.M % d.remap_t ||
                         d.N != d.remap_h * d.remap_d))
     return int(hipErrorInvalidValue);
-  d.splits = d.workspace ? tlh::gemm_choose_splits(d) : 1;
   return tlh::gemm_launch(d, stream);
 }
 

@@ -12,7 +12,8 @@
 //             (+bias +residual) | RMSNorm, vocab GEMM, fused CE fwd+bwd
 //   backward  transposed-operand GEMMs (no materialised transposes),
 //             GELU' fused into the dG GEMM epilogue, fused RMSNorm',
-//             attention backward, split-K weight gradients
+//             attention backward, split-K weight gradients that also emit
+//             the bias gradients
 //   step      one multi-tensor squared norm, one multi-tensor clip+AdamW.
 // Every buffer is allocated once in tlg_create (lifetime planned by hand:
 // activations kept for the backward, one shared scratch set), so the whole
@@ -157,6 +158,15 @@ int timed(Program &p, std::vector<std::pair<void *, void *>> &spans, F &&launch)
   return 0;
 }
 
+// Weight and bias gradient of y = x.W + b: dW = x^T.dy (x stored [rows, in])
+// with db = column sums of dy computed inside the same GEMM.
+tlh_gemm_desc wgrad(const float *x, const float *dy, float *dw, float *db, int in, int out,
+                    int rows) {
+  tlh_gemm_desc d = desc(x, dy, dw, in, out, rows, true, false);
+  d.bias_grad = db;
+  return d;
+}
+
 int gemm(Program &p, tlh_gemm_desc d) {
   if (d.trans_a) d.workspace = p.workspace; // tall-K weight gradients may split K
   if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k;
@@ -218,30 +228,26 @@ int backward(Program &p) {
   const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
   const uint32_t last = 2 + 12 * c.layers;
   // vocab projection
-  TRY(gemm(p, desc(p.nf, p.dlogits, p.G(last), D, V, R, true, false)));
-  TRY(tlh_column_sum(p.dlogits, p.R, c.vocab, p.G(last + 1), 0.0f, p.stream));
+  TRY(gemm(p, wgrad(p.nf, p.dlogits, p.G(last), p.G(last + 1), D, V, R)));
   TRY(gemm(p, desc(p.dlogits, p.P(last), p.tmp, R, D, V, false, true)));
   TRY(tlh_rms_norm_backward(p.tmp, p.x[c.layers], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
                             0.0f, p.stream));
   for (int l = int(c.layers) - 1; l >= 0; --l) {
     const uint32_t w = 2 + 12 * uint32_t(l);
     // FFN: x[l+1] = x_mid + W2.GELU(W1.n2 + b1) + b2
-    TRY(gemm(p, desc(p.g[l], p.dx, p.G(w + 10), F, D, R, true, false)));
-    TRY(tlh_column_sum(p.dx, p.R, c.dim, p.G(w + 11), 0.0f, p.stream));
+    TRY(gemm(p, wgrad(p.g[l], p.dx, p.G(w + 10), p.G(w + 11), F, D, R)));
     {
       tlh_gemm_desc d = desc(p.dx, p.P(w + 10), p.dgf, R, F, D, false, true);
       d.epilogue = TLH_EPI_GELU_BWD;
       d.aux = p.u[l];
       TRY(gemm(p, d));
     }
-    TRY(gemm(p, desc(p.n2[l], p.dgf, p.G(w + 8), D, F, R, true, false)));
-    TRY(tlh_column_sum(p.dgf, p.R, c.ffn, p.G(w + 9), 0.0f, p.stream));
+    TRY(gemm(p, wgrad(p.n2[l], p.dgf, p.G(w + 8), p.G(w + 9), D, F, R)));
     TRY(gemm(p, desc(p.dgf, p.P(w + 8), p.tmp, R, D, F, false, true)));
     TRY(tlh_rms_norm_backward(p.tmp, p.x_mid[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
                               1.0f, p.stream));
     // attention: x_mid = x + Wo.attn(n1) + bo
-    TRY(gemm(p, desc(p.o[l], p.dx, p.G(w + 6), D, D, R, true, false)));
-    TRY(tlh_column_sum(p.dx, p.R, c.dim, p.G(w + 7), 0.0f, p.stream));
+    TRY(gemm(p, wgrad(p.o[l], p.dx, p.G(w + 6), p.G(w + 7), D, D, R)));
     TRY(gemm(p, desc(p.dx, p.P(w + 6), p.tmp, R, D, D, false, true)));
     TRY(timed(p, p.attn_spans, [&] {
       return tlh_attention_backward(p.q[l], p.k[l], p.v[l], p.o[l], p.tmp, p.lse[l], p.delta,
@@ -249,10 +255,8 @@ int backward(Program &p) {
                                     1.0f / std::sqrt(float(kHeadDim)), 1, 1, 1, p.stream);
     }));
     float *dqkv[3] = {p.dq, p.dk, p.dv};
-    for (int j = 0; j < 3; ++j) {
-      TRY(gemm(p, desc(p.n1[l], dqkv[j], p.G(w + 2 * j), D, D, R, true, false)));
-      TRY(tlh_column_sum(dqkv[j], p.R, c.dim, p.G(w + 2 * j + 1), 0.0f, p.stream));
-    }
+    for (int j = 0; j < 3; ++j)
+      TRY(gemm(p, wgrad(p.n1[l], dqkv[j], p.G(w + 2 * j), p.G(w + 2 * j + 1), D, D, R)));
     for (int j = 0; j < 3; ++j) {
       tlh_gemm_desc d = desc(dqkv[j], p.P(w + 2 * j), p.tmp, R, D, D, false, true);
       d.beta = j == 0 ? 0.0f : 1.0f;

@@ -33,6 +33,7 @@ class GemmDesc(ctypes.Structure):
         ("beta", c_float),
         ("epilogue", c_int32),
         ("remap_t", c_int32), ("remap_h", c_int32), ("remap_d", c_int32),
+        ("bias_grad", c_void_p),
     ]
 
 

@@ -158,7 +158,7 @@ def test_matmul_kat_and_identity(g):
 
 
 def gemm(g, a, b, ta=False, tb=False, bias=None, residual=None, epi=0, aux=None, beta=0.0,
-         c_init=None, remap=None, split=True):
+         c_init=None, remap=None, split=True, bias_grad_init=None):
     M = a.shape[1] if ta else a.shape[0]
     K = a.shape[0] if ta else a.shape[1]
     N = b.shape[0] if tb else b.shape[1]
@@ -185,12 +185,17 @@ def gemm(g, a, b, ta=False, tb=False, bias=None, residual=None, epi=0, aux=None,
     d.epilogue = epi
     if remap:
         d.remap_t, d.remap_h, d.remap_d = remap
+    dbg = None
+    if bias_grad_init is not None:
+        dbg = g.dev(bias_grad_init); keep.append(dbg); d.bias_grad = dbg.data_ptr()
     if split:
         n = ctypes.c_size_t()
         g.lib.tlh_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n))
         if n.value:
             ws = g.empty((n.value,)); keep.append(ws); d.workspace = ws.data_ptr()
     g.call("tlh_gemm", ctypes.byref(d))
+    if dbg is not None:
+        return g.host(dc), g.host(dbg)
     return g.host(dc), (g.host(daux) if daux is not None else None)
 
 
@@ -202,6 +207,19 @@ def test_gemm_layouts(g, ta, tb, M, N, K):
     out, _ = gemm(g, a, b, ta, tb)
     expect = O.matmul(a.T if ta else a, b.T if tb else b)
     assert_rel(out.reshape(M, N), expect, 1e-3, "gemm")
+
+
+@pytest.mark.parametrize("M,N,K,split", [(384, 384, 6144, True), (384, 2048, 6144, True),
+                                         (100, 70, 37, True), (384, 384, 6144, False)])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_gemm_weight_grad_fused_bias_grad(g, M, N, K, split, beta):
+    # dW = X^T.dY with db = column sums of dY from the same launch
+    x = O.normal((K, M), 130, 0, 0.5)   # X stored [rows=K, in=M]
+    dy = O.normal((K, N), 131, 0, 0.5)
+    w0, b0 = O.normal((M, N), 132), O.normal((N,), 133)
+    dw, db = gemm(g, x, dy, ta=True, beta=beta, c_init=w0, bias_grad_init=b0, split=split)
+    assert_rel(dw.reshape(M, N), O.matmul(x.T, dy) + beta * w0, 1e-3, "dW")
+    assert_close(db, O.sum_to_shape(dy, [N]) + beta * b0, rtol=1e-4, atol=1e-3, what="db")
 
 
 def test_gemm_bias_residual_beta(g):
