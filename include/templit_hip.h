@@ -95,11 +95,27 @@ int tlh_event_synchronize(void *event);
 int tlh_event_elapsed_ms(void *start, void *end, float *host_ms);
 int tlh_event_destroy(void *event);
 
-/* Command-buffer record/commit as a hipGraph (runtime.cpp:290-309). */
+/* Command-buffer record/commit as a hipGraph (runtime.cpp:290-309).
+ * begin/end_capture: thread-local capture, instantiated on end. */
 int tlh_graph_begin_capture(void *stream);
 int tlh_graph_end_capture(void *stream, void **exec);
 int tlh_graph_launch(void *exec, void *stream);
 int tlh_graph_destroy(void *exec);
+/* Relaxed-mode capture that returns the un-instantiated graph, for callers
+ * (hip::Runtime's graph mode) that cache executable graphs and refresh them
+ * with tlh_graph_exec_update: *updated = 1 when `exec` took `graph`'s
+ * parameters (same topology), 0 when it must be re-instantiated. */
+int tlh_graph_begin_capture_relaxed(void *stream);
+int tlh_graph_end_capture_graph(void *stream, void **graph);
+int tlh_graph_instantiate(void *graph, void **exec);
+int tlh_graph_exec_update(void *exec, void *graph, int *updated);
+int tlh_graph_free(void *graph);
+int tlh_stream_is_capturing(void *stream, int *capturing);
+
+/* Profiling ranges (roctx; seen by rocprofv3 --marker-trace): stand in for
+ * Runtime::start_profile / end_profile (runtime.cpp:42-63). */
+int tlh_range_push(const char *name);
+int tlh_range_pop(void);
 
 /* ---------------------------------------------------------------------------
  * Elementwise (math.metal:401-548, 821-855, 1045-1050)
@@ -298,22 +314,25 @@ int tlh_rms_norm_backward(const float *g, const float *x, const float *gain,
  * ------------------------------------------------------------------------- */
 
 /* embedding_lookup / gather_rows (math.metal:778-793, runtime.cpp:920-950):
- * out[i, :] = weights[ids[i], :]. Bit-exact copy; ids >= rows -> hipErrorInvalidValue
- * is not detected on device: callers validate (reference does not check). */
+ * out[i, :] = weights[ids[i], :], a bit-exact copy. weights is [rows, dim].
+ * The reference reads unchecked; here a row whose id is >= rows is written
+ * as NaN, so a bad id never reads outside the table. */
 int tlh_embedding_lookup(const float *weights, uint32_t rows, uint32_t dim,
                          const uint32_t *ids, size_t n_ids, float *out,
                          void *stream);
 /* Fused token+position embedding: out[b,t,:] = tok[ids[b,t],:] + pos[t,:]
- * (GPT.h:62-64: add(embedding(input), embedding(positions))). */
-int tlh_embedding_add_positions(const float *tok, const float *pos,
+ * (GPT.h:62-64: add(embedding(input), embedding(positions))). tok is
+ * [vocab, dim]; an id >= vocab gives a NaN row. */
+int tlh_embedding_add_positions(const float *tok, uint32_t vocab, const float *pos,
                                 const uint32_t *ids, uint32_t batch,
                                 uint32_t seq, uint32_t dim, float *out,
                                 void *stream);
 /* scatter_add_rows (math.metal:794-820, runtime.cpp:952-981): dst[ids[i],:]
- * += values[i,:] with float atomics (order nondeterministic). The caller
- * pre-fills dst (base copy or zero, runtime.cpp:983-1030). */
+ * += values[i,:] with float atomics (order nondeterministic). dst is
+ * [dst_rows, dim]; ids >= dst_rows are dropped. The caller pre-fills dst
+ * (base copy or zero, runtime.cpp:983-1030). */
 int tlh_scatter_add_rows(const float *values, const uint32_t *ids, size_t n_ids,
-                         uint32_t dim, float *dst, void *stream);
+                         uint32_t dim, float *dst, uint32_t dst_rows, void *stream);
 /* ---------------------------------------------------------------------------
  * Attention (no reference op: replaces the decomposed chain of
  * include/nn/multi_head.h:33-55)

@@ -1,9 +1,11 @@
 """Build recipe for the native parts of templit_amd.
 
 Produces, in-tree (so the built files travel with the source tree):
-  templit_amd/libtemplit_hip.so   hand-written gfx950 HIP kernels + C-ABI
-  templit_amd/libtemplit_gpt.so   GPT step program (host C++ over the C-ABI)
-  tests/cpp/test_hip_runtime      C++ runtime tests (hip::Runtime over the C-ABI)
+  templit_amd/libtemplit_hip.so     hand-written gfx950 HIP kernels + C-ABI
+  templit_amd/libtemplit_runtime.so hip::Runtime / Storage<hip::HIP,T> (host C++
+                                    over the C-ABI)
+  templit_amd/libtemplit_gpt.so     GPT step program (host C++ over the C-ABI)
+  tests/cpp/bin/test_*              C++ tests of the runtime surface
 
 Run:  python -m templit_amd.build   (or __graft_entry__.build()).
 Every call recompiles (objects are cached by content hash of the source
@@ -55,9 +57,17 @@ KERNEL_SOURCES = [
     "optim.hip",
 ]
 
+RUNTIME_SOURCES = [
+    "hip_context.cpp",
+    "runtime.cpp",
+]
+
 GPT_SOURCES = [
     "gpt_program.cpp",
 ]
+
+HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{PKG_INCLUDE}",
+              f"-I{CSRC}"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -83,7 +93,7 @@ def _digest(paths: list[Path], flags: list[str]) -> str:
 
 def _headers() -> list[Path]:
     hs = sorted(CSRC.glob("*.h")) + sorted(INCLUDE.glob("*.h"))
-    hs += sorted(PKG_INCLUDE.rglob("*.h"))
+    hs += sorted(PKG_INCLUDE.rglob("*.h")) + sorted((ROOT / "tests" / "cpp").glob("*.h"))
     return hs
 
 
@@ -105,7 +115,18 @@ def build_kernels(jobs: int = 8) -> Path:
     lib = PKG / "libtemplit_hip.so"
     tmp = PKG / "libtemplit_hip.so.tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *map(str, objs)])
+          *map(str, objs), "-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx",
+          "-Wl,-rpath,/opt/rocm/lib"])
+    tmp.replace(lib)
+    return lib
+
+
+def build_runtime(kernel_lib: Path) -> Path:
+    objs = [_compile(CSRC / s, HOST_FLAGS, "g++") for s in RUNTIME_SOURCES]
+    lib = PKG / "libtemplit_runtime.so"
+    tmp = PKG / "libtemplit_runtime.so.tmp"
+    _run(["g++", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+          f"-L{PKG}", "-ltemplit_hip", "-Wl,-rpath,$ORIGIN"])
     tmp.replace(lib)
     return lib
 
@@ -114,8 +135,7 @@ def build_gpt(kernel_lib: Path) -> Path | None:
     srcs = [CSRC / s for s in GPT_SOURCES if (CSRC / s).exists()]
     if not srcs:
         return None
-    flags = ["-O2", "-std=c++20", "-fPIC", f"-I{INCLUDE}", f"-I{PKG_INCLUDE}", f"-I{CSRC}"]
-    objs = [_compile(s, flags, "g++") for s in srcs]
+    objs = [_compile(s, HOST_FLAGS, "g++") for s in srcs]
     lib = PKG / "libtemplit_gpt.so"
     tmp = PKG / "libtemplit_gpt.so.tmp"
     _run(["g++", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
@@ -124,16 +144,18 @@ def build_gpt(kernel_lib: Path) -> Path | None:
     return lib
 
 
-def build_cpp_tests(kernel_lib: Path) -> list[Path]:
+def build_cpp_tests() -> list[Path]:
     tdir = ROOT / "tests" / "cpp"
+    bindir = tdir / "bin"
+    bindir.mkdir(exist_ok=True)
     out = []
-    for src in sorted(tdir.glob("test_*.cpp")) if tdir.exists() else []:
-        exe = tdir / src.stem
-        flags = ["-O2", "-std=c++20", f"-I{INCLUDE}", f"-I{PKG_INCLUDE}", f"-I{tdir}"]
-        runtime_src = [CSRC / "runtime.cpp"] if (CSRC / "runtime.cpp").exists() else []
-        objs = [_compile(s, flags, "g++") for s in [src, *runtime_src]]
-        _run(["g++", "-o", str(exe), *map(str, objs), f"-L{PKG}", "-ltemplit_hip",
-              f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/../../templit_amd"])
+    for src in sorted(tdir.glob("test_*.cpp")):
+        exe = bindir / src.stem
+        obj = _compile(src, HOST_FLAGS + [f"-I{tdir}"], "g++")
+        tmp = exe.with_suffix(".tmp")
+        _run(["g++", "-o", str(tmp), str(obj), f"-L{PKG}", "-ltemplit_runtime",
+              "-ltemplit_hip", "-Wl,-rpath,$ORIGIN/../../../templit_amd"])
+        tmp.replace(exe)
         out.append(exe)
     return out
 
@@ -154,8 +176,9 @@ def build_all() -> None:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     lib = build_kernels()
+    build_runtime(lib)
     build_gpt(lib)
-    build_cpp_tests(lib)
+    build_cpp_tests()
     clean_stale_objects()
 
 

@@ -8,6 +8,8 @@
 // through these functions, so it builds with any C++20 compiler.
 #include "common.h"
 
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include <mutex>
 
 using namespace tlh;
@@ -249,6 +251,53 @@ TLH_API int tlh_graph_end_capture(void *stream, void **exec) {
   *exec = ge;
   return int(e);
 }
+
+TLH_API int tlh_graph_begin_capture_relaxed(void *stream) {
+  return int(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed));
+}
+
+TLH_API int tlh_graph_end_capture_graph(void *stream, void **graph) {
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
+  *graph = g;
+  return int(e);
+}
+
+TLH_API int tlh_graph_instantiate(void *graph, void **exec) {
+  hipGraphExec_t ge = nullptr;
+  const hipError_t e = hipGraphInstantiate(&ge, static_cast<hipGraph_t>(graph), nullptr, nullptr, 0);
+  *exec = ge;
+  return int(e);
+}
+
+// Rewrites the parameters of `exec` from `graph` when both have the same
+// topology; *updated = 0 (and return 0) when they do not.
+TLH_API int tlh_graph_exec_update(void *exec, void *graph, int *updated) {
+  hipGraphNode_t error_node = nullptr;
+  hipGraphExecUpdateResult result = hipGraphExecUpdateSuccess;
+  const hipError_t e = hipGraphExecUpdate(static_cast<hipGraphExec_t>(exec),
+                                          static_cast<hipGraph_t>(graph), &error_node, &result);
+  *updated = (e == hipSuccess && result == hipGraphExecUpdateSuccess) ? 1 : 0;
+  if (e != hipSuccess) (void)hipGetLastError(); // a refused update is not an error here
+  return 0;
+}
+
+TLH_API int tlh_graph_free(void *graph) {
+  return graph ? int(hipGraphDestroy(static_cast<hipGraph_t>(graph))) : 0;
+}
+
+TLH_API int tlh_stream_is_capturing(void *stream, int *capturing) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(as_stream(stream), &st);
+  *capturing = st == hipStreamCaptureStatusActive ? 1 : 0;
+  return int(e);
+}
+
+// Named ranges for rocprofv3 (--marker-trace) around host-side spans:
+// Runtime::start_profile / end_profile (Metal: a GPU-trace capture,
+// src/my_metal/runtime.cpp:42-63).
+TLH_API int tlh_range_push(const char *name) { return roctxRangePushA(name) < 0 ? 1 : 0; }
+TLH_API int tlh_range_pop(void) { return roctxRangePop() < 0 ? 1 : 0; }
 
 TLH_API int tlh_graph_launch(void *exec, void *stream) {
   return int(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), as_stream(stream)));

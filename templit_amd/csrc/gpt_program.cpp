@@ -176,8 +176,8 @@ int gemm(Program &p, tlh_gemm_desc d) {
 int forward(Program &p) {
   const tlg_config &c = p.cfg;
   const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
-  TRY(tlh_embedding_add_positions(p.P(0), p.P(1), p.tokens, c.batch, c.seq, c.dim, p.x[0],
-                                  p.stream));
+  TRY(tlh_embedding_add_positions(p.P(0), c.vocab, p.P(1), p.tokens, c.batch, c.seq, c.dim,
+                                  p.x[0], p.stream));
   for (uint32_t l = 0; l < c.layers; ++l) {
     const uint32_t w = 2 + 12 * l;
     TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, p.R, c.dim, kRmsEps, p.stream));
@@ -268,7 +268,7 @@ int backward(Program &p) {
   // embeddings: scatter_index for tokens (zero + scatter_add_rows), positions
   // as a column sum over the batch of the [B, T*D] view.
   TRY(tlh_fill_f32(p.G(0), 0.0f, p.size[0], p.stream));
-  TRY(tlh_scatter_add_rows(p.dx, p.tokens, p.R, c.dim, p.G(0), p.stream));
+  TRY(tlh_scatter_add_rows(p.dx, p.tokens, p.R, c.dim, p.G(0), c.vocab, p.stream));
   return tlh_column_sum(p.dx, c.batch, c.seq * c.dim, p.G(1), 0.0f, p.stream);
 }
 

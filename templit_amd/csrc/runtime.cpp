@@ -1,0 +1,779 @@
+// hip::Runtime: host-side validation and dispatch of every runtime op onto
+// the gfx950 kernel library (include/templit_hip.h).
+//
+// Each op follows the validation of its metal::Runtime counterpart in
+// src/my_metal/runtime.cpp (cited per op) so that callers see the same
+// exceptions for the same misuse, then enqueues the kernel(s) on the
+// context stream. Where the Metal runtime composes several kernels
+// (RMS: hadamard+sum+divide+add+sqrt, runtime.cpp:1031-1052; RMSNorm: RMS +
+// divide, 1060-1072) this runtime calls one fused kernel with the same
+// arithmetic. Metal-specific choices that are not semantics (threadgroup
+// geometry, pipeline selection by alignment) have no counterpart here: the
+// kernel library picks MFMA tile shapes and launch geometry for gfx950.
+#include "my_hip/runtime.h"
+
+#include "RTensor/infer_shape.h"
+#include "templit_hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "templit/runnable.h"
+
+namespace hip {
+
+static_assert(templit::Runnable<Runtime::Tensor, Runtime>,
+              "hip::Runtime must provide the passes::Runnable operation surface");
+
+namespace {
+
+using Tensor = Runtime::Tensor;
+using IndexTensor = Runtime::IndexTensor;
+using shape_type = rtensor::shape_type;
+
+constexpr float kRmsEpsilon = 1e-6f; // added inside the sqrt, runtime.cpp:1044-1052
+
+enum Op : uint32_t {
+  kAdd = 1, kAddScalar, kSub, kHadamard, kDivide, kDivideScalar, kPow, kSigmoid, kSqrt, kExp,
+  kGelu, kGeluDerivative, kCopy, kMult, kTranspose, kSplit, kMerge, kSum, kSumToShape,
+  kMaxToShape, kArgmax, kSoftmax, kCrossEntropy, kCrossEntropyDerivative, kRms, kRmsNorm,
+  kEmbedding, kScatterAdd, kScatterIndex, kSquaredNorm, kClip, kAdamW, kRmsNormGain,
+  kSoftmaxDerivative, kGeluBackward, kRmsNormDerivative, kAttention, kAttentionBackward,
+};
+
+template <typename T> const T *in(const RTensor<HIP, T> &t) {
+  if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
+  return t.get_storage()->data();
+}
+template <typename T> T *out(RTensor<HIP, T> &t) {
+  if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
+  return t.get_storage()->data();
+}
+
+void check(int code, const char *what) { detail::check(code, what); }
+
+// Element strides of `shape`/`strides` right-aligned to `out_shape`, 0 on
+// broadcast dims (runtime.cpp:18-39).
+std::vector<uint32_t> broadcast_strides(std::span<const uint32_t> shape,
+                                        std::span<const uint32_t> strides,
+                                        std::span<const uint32_t> out_shape) {
+  if (shape.size() > out_shape.size()) throw std::runtime_error("invalid broadcast");
+  std::vector<uint32_t> result(out_shape.size(), 0);
+  const size_t offset = out_shape.size() - shape.size();
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == out_shape[offset + i]) result[offset + i] = strides[i];
+    else if (shape[i] != 1) throw std::runtime_error("invalid broadcast");
+  }
+  return result;
+}
+
+using BinaryFn = int (*)(const float *, const float *, float *, uint32_t, const uint32_t *,
+                         const uint32_t *, const uint32_t *, void *);
+using UnaryFn = int (*)(const float *, float *, size_t, void *);
+using ScalarFn = int (*)(const float *, float, float *, size_t, void *);
+
+void require_same_count(const Tensor &a, const Tensor &o, const char *op) {
+  if (a.numel() != o.numel())
+    throw std::invalid_argument(std::string(op) + " destination has incorrect shape");
+}
+
+// rows x cols view of a tensor whose last dim is the row.
+struct Rows {
+  size_t rows;
+  uint32_t cols;
+};
+Rows as_rows(const Tensor &t, const char *op) {
+  if (t.shape().empty() || t.shape().back() == 0)
+    throw std::invalid_argument(std::string(op) + " requires a non-empty final dimension");
+  return {t.numel() / t.shape().back(), t.shape().back()};
+}
+
+// Drops unit batch dims and merges neighbours that are contiguous in all
+// three operands, so the kernel's 4 batch dims cover any practical rank.
+struct Batch {
+  std::vector<uint32_t> shape, sa, sb, sc;
+};
+Batch simplify_batch(std::span<const uint32_t> shape, const std::vector<uint32_t> &sa,
+                     const std::vector<uint32_t> &sb, std::span<const uint32_t> sc) {
+  Batch out;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == 1) continue;
+    if (!out.shape.empty()) {
+      const size_t j = out.shape.size() - 1;
+      const auto merges = [&](uint32_t outer, uint32_t inner) {
+        return uint64_t(outer) == uint64_t(inner) * shape[i];
+      };
+      if (merges(out.sa[j], sa[i]) && merges(out.sb[j], sb[i]) && merges(out.sc[j], sc[i])) {
+        out.shape[j] *= shape[i];
+        out.sa[j] = sa[i];
+        out.sb[j] = sb[i];
+        out.sc[j] = sc[i];
+        continue;
+      }
+    }
+    out.shape.push_back(shape[i]);
+    out.sa.push_back(sa[i]);
+    out.sb.push_back(sb[i]);
+    out.sc.push_back(sc[i]);
+  }
+  return out;
+}
+
+} // namespace
+
+struct Runtime::State {
+  bool recording = false;
+  bool submitted = false;
+  bool graph_mode = false;
+  bool capturing = false;
+  bool profiling = false;
+  uint64_t signature = 0;
+  std::unordered_map<uint64_t, void *> graphs; // op/shape sequence -> executable graph
+  void *launched = nullptr;
+  GraphStats stats;
+};
+
+Runtime::Runtime() : state_(std::make_unique<State>()) {
+  if (!initialised()) throw std::logic_error("HIP must be initialised before Runtime");
+}
+
+Runtime::~Runtime() { cleanup(); }
+
+void Runtime::require_recording(const char *op) const {
+  if (!state_->recording)
+    throw std::logic_error(std::string("HIP runtime execution has not started (") + op + ")");
+}
+
+// FNV-1a over the op and its output shape: the key of a recorded sequence.
+void Runtime::note(uint32_t op, std::span<const uint32_t> shape) {
+  if (!state_->capturing) return;
+  uint64_t h = state_->signature;
+  const auto mix = [&h](uint64_t v) {
+    h ^= v;
+    h *= 0x100000001b3ull;
+  };
+  mix(op);
+  mix(shape.size());
+  for (uint32_t d : shape) mix(d);
+  state_->signature = h;
+}
+
+// ---- lifecycle (runtime.cpp:170-317) ----------------------------------------
+
+void Runtime::start() {
+  State &s = *state_;
+  if (s.recording || s.submitted) throw std::logic_error("HIP runtime execution already started");
+  if (s.graph_mode) {
+    // Host transfers made while recording happen at record time; nothing
+    // queued earlier may still be running when they do.
+    check(tlh_stream_synchronize(stream()), "hipStreamSynchronize");
+    check(tlh_graph_begin_capture_relaxed(stream()), "hipStreamBeginCapture");
+    s.capturing = true;
+    s.signature = 0xcbf29ce484222325ull;
+  }
+  s.recording = true;
+}
+
+void Runtime::submit() {
+  State &s = *state_;
+  if (!s.recording) throw std::logic_error("HIP runtime execution has not started");
+  s.recording = false;
+  s.submitted = true;
+  if (!s.capturing) return;
+  s.capturing = false;
+  void *graph = nullptr;
+  int st = tlh_graph_end_capture_graph(stream(), &graph);
+  if (st != 0) {
+    s.submitted = false;
+    check(st, "hipStreamEndCapture");
+  }
+  s.stats.captures += 1;
+  void *&exec = s.graphs[s.signature];
+  int updated = 0;
+  if (exec) {
+    st = tlh_graph_exec_update(exec, graph, &updated);
+    if (st == 0 && updated) s.stats.updates += 1;
+  }
+  if (st == 0 && !updated) {
+    if (exec) tlh_graph_destroy(exec);
+    exec = nullptr;
+    st = tlh_graph_instantiate(graph, &exec);
+    if (st == 0) s.stats.instantiations += 1;
+  }
+  tlh_graph_free(graph);
+  if (st == 0) st = tlh_graph_launch(exec, stream());
+  if (st != 0) {
+    s.submitted = false;
+    check(st, "hipGraphLaunch");
+  }
+}
+
+void Runtime::wait() {
+  State &s = *state_;
+  if (!s.submitted || s.recording)
+    throw std::logic_error("HIP runtime execution has not been submitted");
+  s.submitted = false;
+  check(tlh_stream_synchronize(stream()), "HIP runtime execution");
+}
+
+void Runtime::abort() noexcept {
+  State &s = *state_;
+  if (s.capturing) {
+    void *graph = nullptr;
+    if (tlh_graph_end_capture_graph(stream(), &graph) == 0) tlh_graph_free(graph);
+    s.capturing = false;
+  }
+  s.recording = false;
+  s.submitted = false;
+}
+
+void Runtime::cleanup() noexcept {
+  if (!state_) return;
+  State &s = *state_;
+  const bool had_work = s.recording || s.submitted;
+  abort();
+  if (had_work && initialised()) tlh_stream_synchronize(stream());
+  for (auto &[key, exec] : s.graphs) tlh_graph_destroy(exec);
+  s.graphs.clear();
+  if (s.profiling) {
+    tlh_range_pop();
+    s.profiling = false;
+  }
+}
+
+void Runtime::start_profile(std::string_view output_path) {
+  if (state_->profiling) throw std::logic_error("a profile span is already open");
+  const std::string name(output_path);
+  check(tlh_range_push(name.c_str()), "roctxRangePush");
+  state_->profiling = true;
+}
+
+void Runtime::end_profile() {
+  if (!state_->profiling) return;
+  tlh_range_pop();
+  state_->profiling = false;
+}
+
+void Runtime::set_graph_mode(bool enabled) {
+  if (state_->recording || state_->submitted)
+    throw std::logic_error("graph mode can only change between executions");
+  state_->graph_mode = enabled;
+}
+bool Runtime::graph_mode() const { return state_->graph_mode; }
+Runtime::GraphStats Runtime::graph_stats() const { return state_->stats; }
+
+// ---- elementwise (runtime.cpp:65-136, 321-373, 1073-1081, 1170-1186) -------
+
+namespace {
+void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn, const char *what) {
+  const auto sa = broadcast_strides(a.shape(), a.strides(), o.shape());
+  const auto sb = broadcast_strides(b.shape(), b.strides(), o.shape());
+  if (o.numel() == 0) return;
+  check(fn(in(a), in(b), out(o), uint32_t(o.shape().size()), o.shape().data(), sa.data(),
+           sb.data(), stream()),
+        what);
+}
+
+void unary(const Tensor &a, Tensor &o, UnaryFn fn, const char *what) {
+  require_same_count(a, o, what);
+  if (o.numel() == 0) return;
+  check(fn(in(a), out(o), o.numel(), stream()), what);
+}
+
+void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *what) {
+  if (a.shape() != o.shape())
+    throw std::invalid_argument("scalar operation input and output shapes must match");
+  if (o.numel() == 0) return;
+  check(fn(in(a), v, out(o), o.numel(), stream()), what);
+}
+} // namespace
+
+void Runtime::add(const Tensor &a, const Tensor &b, Tensor &o) {
+  require_recording("add");
+  note(kAdd, o.shape());
+  binary(*this, a, b, o, tlh_add, "add");
+}
+void Runtime::sub(const Tensor &a, const Tensor &b, Tensor &o) {
+  require_recording("sub");
+  note(kSub, o.shape());
+  binary(*this, a, b, o, tlh_sub, "sub");
+}
+void Runtime::hadamard(const Tensor &a, const Tensor &b, Tensor &o) {
+  require_recording("hadamard");
+  note(kHadamard, o.shape());
+  binary(*this, a, b, o, tlh_hadamard, "hadamard");
+}
+void Runtime::divide(const Tensor &a, const Tensor &b, Tensor &o) {
+  require_recording("divide");
+  note(kDivide, o.shape());
+  binary(*this, a, b, o, tlh_divide, "divide");
+}
+void Runtime::add(const Tensor &a, kernel_type v, Tensor &o) {
+  require_recording("add");
+  note(kAddScalar, o.shape());
+  scalar_op(a, v, o, tlh_add_scalar, "add_scalar");
+}
+void Runtime::divide(const Tensor &a, kernel_type v, Tensor &o) {
+  require_recording("divide");
+  note(kDivideScalar, o.shape());
+  scalar_op(a, v, o, tlh_divide_scalar, "divide_scalar");
+}
+void Runtime::pow(const Tensor &a, kernel_type v, Tensor &o) {
+  require_recording("pow");
+  note(kPow, o.shape());
+  scalar_op(a, v, o, tlh_pow_scalar, "pow_scalar");
+}
+void Runtime::sigmoid(const Tensor &a, Tensor &o) {
+  require_recording("sigmoid");
+  note(kSigmoid, o.shape());
+  unary(a, o, tlh_sigmoid, "sigmoid");
+}
+void Runtime::sqrt(const Tensor &a, Tensor &o) {
+  require_recording("sqrt");
+  note(kSqrt, o.shape());
+  unary(a, o, tlh_sqrt, "sqrt");
+}
+void Runtime::exp(const Tensor &a, Tensor &o) {
+  require_recording("exp");
+  note(kExp, o.shape());
+  unary(a, o, tlh_exp, "exp");
+}
+void Runtime::GELU(const Tensor &a, Tensor &o) {
+  require_recording("GELU");
+  note(kGelu, o.shape());
+  unary(a, o, tlh_gelu, "GELU");
+}
+void Runtime::GELU_derivative(const Tensor &a, Tensor &o) {
+  require_recording("GELU_derivative");
+  note(kGeluDerivative, o.shape());
+  unary(a, o, tlh_gelu_derivative, "GELU_derivative");
+}
+
+void Runtime::copy(const Tensor &a, Tensor &o) {
+  require_recording("copy");
+  if (a.shape() != o.shape()) throw std::invalid_argument("copy destination has incorrect shape");
+  note(kCopy, o.shape());
+  if (o.numel() == 0 || in(a) == out(o)) return;
+  check(tlh_copy(in(a), out(o), o.numel(), stream()), "copy");
+}
+
+// sub then in-place hadamard (runtime.cpp:843-848).
+void Runtime::sqe(const Tensor &prediction, const Tensor &target, Tensor &o) {
+  sub(prediction, target, o);
+  hadamard(o, o, o);
+}
+
+// ---- products and layout ----------------------------------------------------
+
+// Batched broadcasting matmul (runtime.cpp:375-505) on the fp32 MFMA GEMM.
+void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
+  require_recording("mult");
+  const shape_type expected = rtensor::infer_mult(a.shape(), b.shape());
+  if (o.shape() != expected) throw std::invalid_argument("matmul destination has incorrect shape");
+  note(kMult, o.shape());
+  const size_t ra = a.shape().size(), rb = b.shape().size(), ro = o.shape().size();
+  const uint32_t M = a.shape()[ra - 2], K = a.shape()[ra - 1], N = b.shape()[rb - 1];
+  const std::span<const uint32_t> out_batch(o.shape().data(), ro - 2);
+  const auto sa = broadcast_strides(std::span(a.shape()).first(ra - 2),
+                                    std::span(a.strides()).first(ra - 2), out_batch);
+  const auto sb = broadcast_strides(std::span(b.shape()).first(rb - 2),
+                                    std::span(b.strides()).first(rb - 2), out_batch);
+  const Batch batch =
+      simplify_batch(out_batch, sa, sb, std::span(o.strides()).first(ro - 2));
+  if (batch.shape.size() > 4)
+    throw std::invalid_argument("matmul supports at most 4 non-mergeable batch dimensions");
+  if (o.numel() == 0) return;
+  if (K == 0) { // empty inner dimension: the product is all zeros
+    check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "mult");
+    return;
+  }
+  check(tlh_matmul(in(a), in(b), out(o), M, K, N, a.strides()[ra - 2], a.strides()[ra - 1],
+                   b.strides()[rb - 2], b.strides()[rb - 1], o.strides()[ro - 2],
+                   o.strides()[ro - 1], uint32_t(batch.shape.size()), batch.shape.data(),
+                   batch.sa.data(), batch.sb.data(), batch.sc.data(), stream()),
+        "mult");
+}
+
+// Materialised swap of two dims (runtime.cpp:529-569).
+void Runtime::transpose(const Tensor &a, Tensor &o, int32_t dim_a, int32_t dim_b) {
+  require_recording("transpose");
+  if (a.shape().size() < 2) throw std::invalid_argument("transpose requires rank >= 2");
+  const size_t x = rtensor::normalise_dimension(a.shape().size(), dim_a);
+  const size_t y = rtensor::normalise_dimension(a.shape().size(), dim_b);
+  if (x == y) throw std::invalid_argument("transpose dimensions must be different");
+  if (o.shape() != rtensor::infer_transpose(a.shape(), dim_a, dim_b))
+    throw std::invalid_argument("transpose destination has incorrect shape");
+  if (a.shape().size() > 8) throw std::invalid_argument("transpose supports rank <= 8");
+  note(kTranspose, o.shape());
+  if (o.numel() == 0) return;
+  shape_type strides = a.strides();
+  std::swap(strides[x], strides[y]);
+  check(tlh_transpose(in(a), out(o), uint32_t(o.shape().size()), o.shape().data(),
+                      strides.data(), stream()),
+        "transpose");
+}
+
+// The Metal runtime copies a contiguous view into the destination
+// (runtime.cpp:571-593); the bytes do not move, so this is one device copy.
+void Runtime::split_last_dim(const Tensor &a, Tensor &o, uint32_t outer, uint32_t inner) {
+  require_recording("split_last_dim");
+  if (o.shape() != rtensor::infer_split_last_dim(a.shape(), outer, inner))
+    throw std::invalid_argument("split_last_dim destination has incorrect shape");
+  note(kSplit, o.shape());
+  if (o.numel() && in(a) != out(o)) check(tlh_copy(in(a), out(o), o.numel(), stream()), "split");
+}
+
+void Runtime::merge_last_dims(const Tensor &a, Tensor &o, uint32_t outer, uint32_t inner) {
+  require_recording("merge_last_dims");
+  if (o.shape() != rtensor::infer_merge_last_dims(a.shape(), outer, inner))
+    throw std::invalid_argument("merge_last_dims destination has incorrect shape");
+  note(kMerge, o.shape());
+  if (o.numel() && in(a) != out(o)) check(tlh_copy(in(a), out(o), o.numel(), stream()), "merge");
+}
+
+// ---- reductions ----------------------------------------------------------------
+
+void Runtime::sum(const Tensor &a, Tensor &o) { // runtime.cpp:506-518
+  require_recording("sum");
+  if (o.numel() != 1) throw std::invalid_argument("sum destination must hold one element");
+  note(kSum, a.shape());
+  check(tlh_sum(in(a), a.numel(), out(o), stream()), "sum");
+}
+
+void Runtime::sum(const Tensor &a, size_t axis, Tensor &o) { // runtime.cpp:520-527
+  require_recording("sum");
+  if (axis >= a.shape().size()) throw std::out_of_range("sum axis out of range");
+  sum_to_shape(a, o.shape(), o);
+}
+
+// runtime.cpp:661-739: reduce every dim where the (right-aligned) target is
+// 1 and the input is not; leading dims beyond the target's rank are reduced
+// away; no reduced dim means a copy.
+void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Tensor &o) {
+  require_recording("sum_to_shape");
+  const auto &as = a.shape();
+  if (shape.size() > as.size())
+    throw std::invalid_argument("cannot reduce to a shape with a higher rank");
+  if (o.shape().size() != shape.size() || !std::equal(shape.begin(), shape.end(), o.shape().begin()))
+    throw std::invalid_argument("sum_to_shape destination has incorrect shape");
+  shape_type aligned(as.size(), 1);
+  std::copy(shape.begin(), shape.end(), aligned.begin() + (as.size() - shape.size()));
+  bool reduces = false;
+  for (size_t i = 0; i < as.size(); ++i) {
+    if (as[i] == aligned[i]) continue;
+    if (aligned[i] != 1) throw std::invalid_argument("invalid reduce_to_shape");
+    reduces = true;
+  }
+  if (as.size() > 8) throw std::invalid_argument("sum_to_shape supports rank <= 8");
+  note(kSumToShape, o.shape());
+  if (a.numel() == 0) {
+    if (o.numel()) check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "sum_to_shape");
+    return;
+  }
+  if (!reduces) {
+    if (in(a) != out(o)) check(tlh_copy(in(a), out(o), o.numel(), stream()), "sum_to_shape");
+    return;
+  }
+  check(tlh_sum_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(), stream()),
+        "sum_to_shape");
+}
+
+// reduce_to_shape with the max kernel (runtime.cpp:595-659, 741-745): same
+// rank, at most one shrinking dim; nothing to shrink aliases the input.
+void Runtime::max_to_shape(const Tensor &a, std::span<const uint32_t> shape, Tensor &o) {
+  require_recording("max_to_shape");
+  const auto &as = a.shape();
+  if (shape.size() != as.size()) throw std::invalid_argument("cannot reduce to shape if ranks differ");
+  size_t shrinking = 0;
+  for (size_t i = 0; i < as.size(); ++i) {
+    if (as[i] == shape[i]) continue;
+    if (shape[i] != 1) throw std::invalid_argument("invalid reduce_to_shape");
+    if (++shrinking > 1)
+      throw std::invalid_argument("reduce_to_shape currently supports only one shrinking dimension");
+  }
+  if (shrinking == 0) {
+    o = a;
+    return;
+  }
+  if (o.shape().size() != shape.size() || !std::equal(shape.begin(), shape.end(), o.shape().begin()))
+    throw std::invalid_argument("max_to_shape destination has incorrect shape");
+  if (as.size() > 8) throw std::invalid_argument("max_to_shape supports rank <= 8");
+  note(kMaxToShape, o.shape());
+  if (o.numel() == 0) return;
+  check(tlh_max_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), shape.data(), stream()),
+        "max_to_shape");
+}
+
+// Index of the first maximum (runtime.cpp:850-918).
+void Runtime::argmax(const Tensor &a, IndexTensor &o) {
+  require_recording("argmax");
+  if (a.numel() == 0) throw std::invalid_argument("argmax requires a non-empty tensor");
+  if (o.numel() != 1) throw std::invalid_argument("argmax destination must hold one index");
+  note(kArgmax, a.shape());
+  check(tlh_argmax(in(a), a.numel(), out(o), stream()), "argmax");
+}
+
+// ---- row ops -----------------------------------------------------------------------
+
+void Runtime::softmax(const Tensor &x, Tensor &o) { // runtime.cpp:747-766
+  require_recording("softmax");
+  const Rows r = as_rows(x, "softmax");
+  if (o.shape() != x.shape()) throw std::invalid_argument("softmax destination has incorrect shape");
+  note(kSoftmax, o.shape());
+  check(tlh_softmax(in(x), out(o), r.rows, r.cols, stream()), "softmax");
+}
+
+void Runtime::cross_entropy(const Tensor &logits, const IndexTensor &targets, Tensor &o) {
+  require_recording("cross_entropy"); // runtime.cpp:768-804
+  const shape_type expected = rtensor::infer_cross_entropy(logits.shape(), targets.shape());
+  if (o.shape() != expected)
+    throw std::invalid_argument("cross_entropy destination must match target shape with a "
+                                "trailing singleton dimension");
+  note(kCrossEntropy, logits.shape());
+  const Rows r = as_rows(logits, "cross_entropy");
+  if (r.rows == 0) return;
+  check(tlh_cross_entropy_rows(in(logits), in(targets), out(o), r.rows, r.cols, stream()),
+        "cross_entropy");
+}
+
+void Runtime::cross_entropy_derivative(const Tensor &logits, const IndexTensor &targets,
+                                       Tensor &o) { // runtime.cpp:806-841
+  require_recording("cross_entropy_derivative");
+  (void)rtensor::infer_cross_entropy(logits.shape(), targets.shape());
+  if (o.shape() != logits.shape())
+    throw std::invalid_argument("cross_entropy_derivative destination must match logits shape");
+  note(kCrossEntropyDerivative, o.shape());
+  const Rows r = as_rows(logits, "cross_entropy_derivative");
+  if (r.rows == 0) return;
+  check(tlh_cross_entropy_rows_backward(in(logits), in(targets), out(o), r.rows, r.cols, nullptr,
+                                        stream()),
+        "cross_entropy_derivative");
+}
+
+void Runtime::RMS(const Tensor &a, Tensor &o) { // runtime.cpp:1031-1058
+  require_recording("RMS");
+  RMS_impl(a, o);
+}
+
+void Runtime::RMS_impl(const Tensor &a, Tensor &o) {
+  if (a.shape().empty()) throw std::invalid_argument("RMS requires rank >= 1");
+  if (o.shape() != rtensor::infer_rms(a.shape()))
+    throw std::invalid_argument("RMS destination has incorrect shape");
+  note(kRms, a.shape());
+  if (a.numel() == 0) return;
+  check(tlh_rms(in(a), out(o), a.numel() / a.shape().back(), a.shape().back(), kRmsEpsilon,
+                stream()),
+        "RMS");
+}
+
+void Runtime::RMSNorm(const Tensor &a, Tensor &o) { // runtime.cpp:1060-1072
+  require_recording("RMSNorm");
+  if (o.shape() != a.shape()) throw std::invalid_argument("RMSNorm destination has incorrect shape");
+  if (a.shape().empty()) throw std::invalid_argument("RMSNorm requires rank >= 1");
+  note(kRmsNorm, a.shape());
+  if (a.numel() == 0) return;
+  check(tlh_rms_norm(in(a), nullptr, out(o), nullptr, a.numel() / a.shape().back(),
+                     a.shape().back(), kRmsEpsilon, stream()),
+        "RMSNorm");
+}
+
+// ---- embedding (runtime.cpp:920-1030) ------------------------------------------------
+
+void Runtime::embedding_lookup(const Tensor &w, const IndexTensor &ids, Tensor &o) {
+  require_recording("embedding_lookup");
+  if (w.shape().size() != 2) throw std::invalid_argument("embedding weights must have rank 2");
+  shape_type expected = ids.shape();
+  expected.push_back(w.shape().back());
+  if (o.shape() != expected) throw std::invalid_argument("embedding output shape does not match IDs");
+  note(kEmbedding, o.shape());
+  if (o.numel() == 0) return;
+  check(tlh_embedding_lookup(in(w), w.shape()[0], w.shape()[1], in(ids), ids.numel(), out(o),
+                             stream()),
+        "embedding_lookup");
+}
+
+void Runtime::gather_rows(const Tensor &values, const IndexTensor &ids, Tensor &o) {
+  embedding_lookup(values, ids, o);
+}
+
+namespace {
+void validate_scatter(const Tensor &values, const IndexTensor &ids, const Tensor &dst) {
+  if (dst.shape().size() != 2) throw std::invalid_argument("scatter destination must have rank 2");
+  shape_type expected = ids.shape();
+  expected.push_back(dst.shape().back());
+  if (values.shape() != expected)
+    throw std::invalid_argument("scatter input shape does not match IDs and embedding size");
+}
+void scatter(const Tensor &values, const IndexTensor &ids, Tensor &dst) {
+  if (values.numel() == 0) return;
+  check(tlh_scatter_add_rows(in(values), in(ids), ids.numel(), dst.shape()[1], out(dst),
+                             dst.shape()[0], stream()),
+        "scatter_add_rows");
+}
+} // namespace
+
+void Runtime::scatter_add_rows(const Tensor &base, const IndexTensor &ids, const Tensor &values,
+                               Tensor &o) {
+  require_recording("scatter_add_rows");
+  if (base.shape() != o.shape())
+    throw std::invalid_argument("scatter base and destination shapes must match");
+  validate_scatter(values, ids, o);
+  note(kScatterAdd, o.shape());
+  if (o.numel() && in(base) != out(o))
+    check(tlh_copy(in(base), out(o), o.numel(), stream()), "scatter_add_rows");
+  scatter(values, ids, o);
+}
+
+void Runtime::scatter_index(const Tensor &values, const IndexTensor &ids, Tensor &o) {
+  require_recording("scatter_index");
+  validate_scatter(values, ids, o);
+  note(kScatterIndex, o.shape());
+  if (o.numel()) check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "scatter_index");
+  scatter(values, ids, o);
+}
+
+// ---- optimiser (runtime.cpp:1083-1168) -----------------------------------------------------
+
+void Runtime::accumulate_gradient_squared_norm(const Tensor &g, Tensor &s) {
+  require_recording("accumulate_gradient_squared_norm");
+  if (s.numel() != 1) throw std::invalid_argument("gradient norm destination must be a scalar");
+  note(kSquaredNorm, g.shape());
+  if (g.numel() == 0) return;
+  check(tlh_accumulate_gradient_squared_norm(in(g), g.numel(), out(s), stream()),
+        "accumulate_gradient_squared_norm");
+}
+
+void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_norm, Tensor &o) {
+  require_recording("clip_gradient");
+  if (s.numel() != 1) throw std::invalid_argument("gradient norm input must be a scalar");
+  if (g.shape() != o.shape())
+    throw std::invalid_argument("gradient clipping input and destination shapes must match");
+  if (!(max_norm > 0.0f) || !std::isfinite(max_norm))
+    throw std::invalid_argument("maximum gradient norm must be finite and positive");
+  note(kClip, g.shape());
+  if (g.numel() == 0) return;
+  check(tlh_clip_gradient(in(g), in(s), max_norm, out(o), g.numel(), stream()), "clip_gradient");
+}
+
+void Runtime::adamW(const Tensor &p, const Tensor &g, Tensor &o, Tensor &m1, Tensor &m2,
+                    const Tensor &beta1, const Tensor &beta2, const Tensor &decay,
+                    const Tensor &lr, kernel_type epsilon, uint32_t step) {
+  require_recording("adamW");
+  if (g.shape() != p.shape() || o.shape() != p.shape() || m1.shape() != p.shape() ||
+      m2.shape() != p.shape())
+    throw std::invalid_argument("AdamW tensor shapes must match");
+  if (beta1.numel() != 1 || beta2.numel() != 1 || decay.numel() != 1 || lr.numel() != 1)
+    throw std::invalid_argument("AdamW parameters must be scalars");
+  if (step == 0) throw std::invalid_argument("AdamW step must be greater than zero");
+  note(kAdamW, p.shape());
+  if (p.numel() == 0) return;
+  check(tlh_adamw(in(p), in(g), out(o), out(m1), out(m2), in(beta1), in(beta2), in(decay), in(lr),
+                  epsilon, step, p.numel(), stream()),
+        "adamW");
+}
+
+// ---- fused extensions ---------------------------------------------------------------------------
+
+void Runtime::RMSNorm(const Tensor &a, const Tensor &gain, kernel_type epsilon, Tensor &o) {
+  require_recording("RMSNorm");
+  if (o.shape() != a.shape()) throw std::invalid_argument("RMSNorm destination has incorrect shape");
+  const Rows r = as_rows(a, "RMSNorm");
+  const bool has_gain = gain.get_storage() != nullptr;
+  if (has_gain && gain.numel() != r.cols)
+    throw std::invalid_argument("RMSNorm gain must have one value per column");
+  note(kRmsNormGain, a.shape());
+  if (r.rows == 0) return;
+  check(tlh_rms_norm(in(a), has_gain ? in(gain) : nullptr, out(o), nullptr, r.rows, r.cols,
+                     epsilon, stream()),
+        "RMSNorm");
+}
+
+void Runtime::softmax_derivative(const Tensor &grad, const Tensor &y, Tensor &o) {
+  require_recording("softmax_derivative");
+  if (grad.shape() != y.shape() || o.shape() != y.shape())
+    throw std::invalid_argument("softmax_derivative shapes must match");
+  const Rows r = as_rows(y, "softmax_derivative");
+  note(kSoftmaxDerivative, y.shape());
+  if (r.rows == 0) return;
+  check(tlh_softmax_backward(in(grad), in(y), out(o), r.rows, r.cols, stream()),
+        "softmax_derivative");
+}
+
+void Runtime::GELU_backward(const Tensor &grad, const Tensor &x, Tensor &o) {
+  require_recording("GELU_backward");
+  if (grad.shape() != x.shape() || o.shape() != x.shape())
+    throw std::invalid_argument("GELU_backward shapes must match");
+  note(kGeluBackward, x.shape());
+  if (x.numel() == 0) return;
+  check(tlh_gelu_backward(in(grad), in(x), out(o), x.numel(), stream()), "GELU_backward");
+}
+
+void Runtime::RMSNorm_derivative(const Tensor &grad, const Tensor &x, Tensor &o) {
+  require_recording("RMSNorm_derivative");
+  if (grad.shape() != x.shape() || o.shape() != x.shape())
+    throw std::invalid_argument("RMSNorm_derivative shapes must match");
+  const Rows r = as_rows(x, "RMSNorm_derivative");
+  note(kRmsNormDerivative, x.shape());
+  if (r.rows == 0) return;
+  check(tlh_rms_norm_backward(in(grad), in(x), nullptr, out(o), nullptr, r.rows, r.cols,
+                              kRmsEpsilon, 0.0f, stream()),
+        "RMSNorm_derivative");
+}
+
+namespace {
+struct AttentionDims {
+  uint32_t b, h, t, d;
+};
+AttentionDims attention_dims(const Tensor &q, const Tensor &k, const Tensor &v) {
+  if (q.shape().size() != 4 || k.shape() != q.shape() || v.shape() != q.shape())
+    throw std::invalid_argument("attention operands must all be [B, H, T, 64]");
+  const AttentionDims d{q.shape()[0], q.shape()[1], q.shape()[2], q.shape()[3]};
+  if (d.d != 64) throw std::invalid_argument("attention head dimension must be 64");
+  return d;
+}
+void require_lse(const Tensor &lse, const AttentionDims &d) {
+  if (lse.numel() != size_t(d.b) * d.h * d.t)
+    throw std::invalid_argument("attention log-sum-exp must hold B*H*T values");
+}
+} // namespace
+
+void Runtime::causal_attention(const Tensor &q, const Tensor &k, const Tensor &v, kernel_type scale,
+                               Tensor &o, Tensor &lse) {
+  require_recording("causal_attention");
+  const AttentionDims d = attention_dims(q, k, v);
+  if (o.shape() != q.shape()) throw std::invalid_argument("attention output has incorrect shape");
+  require_lse(lse, d);
+  note(kAttention, q.shape());
+  if (q.numel() == 0) return;
+  check(tlh_attention_forward(in(q), in(k), in(v), out(o), out(lse), d.b, d.h, d.t, d.d, scale, 1,
+                              0, stream()),
+        "causal_attention");
+}
+
+void Runtime::causal_attention_backward(const Tensor &q, const Tensor &k, const Tensor &v,
+                                        const Tensor &o, const Tensor &grad_out, const Tensor &lse,
+                                        kernel_type scale, Tensor &grad_q, Tensor &grad_k,
+                                        Tensor &grad_v) {
+  require_recording("causal_attention_backward");
+  const AttentionDims d = attention_dims(q, k, v);
+  if (o.shape() != q.shape() || grad_out.shape() != q.shape() || grad_q.shape() != q.shape() ||
+      grad_k.shape() != q.shape() || grad_v.shape() != q.shape())
+    throw std::invalid_argument("attention gradients must match the operands' shape");
+  require_lse(lse, d);
+  note(kAttentionBackward, q.shape());
+  if (q.numel() == 0) return;
+  // Per-row dot(dO, O) workspace; freed to the pool right away, which is
+  // safe because its next user is ordered after this work on the stream.
+  Tensor delta({d.b, d.h, d.t});
+  check(tlh_attention_backward(in(q), in(k), in(v), in(o), in(grad_out), in(lse), out(delta),
+                               out(grad_q), out(grad_k), out(grad_v), d.b, d.h, d.t, d.d, scale, 1,
+                               0, 0, stream()),
+        "causal_attention_backward");
+}
+
+} // namespace hip

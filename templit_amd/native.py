@@ -69,6 +69,14 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_graph_end_capture": [P, POINTER(c_void_p)],
     "tlh_graph_launch": [P, P],
     "tlh_graph_destroy": [P],
+    "tlh_graph_begin_capture_relaxed": [P],
+    "tlh_graph_end_capture_graph": [P, POINTER(c_void_p)],
+    "tlh_graph_instantiate": [P, POINTER(c_void_p)],
+    "tlh_graph_exec_update": [P, P, POINTER(c_int)],
+    "tlh_graph_free": [P],
+    "tlh_stream_is_capturing": [P, POINTER(c_int)],
+    "tlh_range_push": [ctypes.c_char_p],
+    "tlh_range_pop": [],
     # elementwise
     "tlh_add": [P, P, P, c_uint32, U32P, U32P, U32P, P],
     "tlh_sub": [P, P, P, c_uint32, U32P, U32P, U32P, P],
@@ -110,8 +118,8 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_rms_norm_backward": [P, P, P, P, P, c_size_t, c_uint32, c_float, c_float, P],
     # embedding
     "tlh_embedding_lookup": [P, c_uint32, c_uint32, P, c_size_t, P, P],
-    "tlh_embedding_add_positions": [P, P, P, c_uint32, c_uint32, c_uint32, P, P],
-    "tlh_scatter_add_rows": [P, P, c_size_t, c_uint32, P, P],
+    "tlh_embedding_add_positions": [P, c_uint32, P, P, c_uint32, c_uint32, c_uint32, P, P],
+    "tlh_scatter_add_rows": [P, P, c_size_t, c_uint32, P, c_uint32, P],
     # attention
     "tlh_attention_forward": [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32,
                               c_float, c_int, c_int, P],

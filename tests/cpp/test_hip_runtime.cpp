@@ -1,0 +1,647 @@
+// hip::Runtime on the GPU: the known-answer tests the reference holds for
+// its Metal runtime (tests/test_metal_runtime.cpp:83-658, values restated
+// here), the host-side validation the executor relies on (exception types
+// for misuse), in-place use, graph mode, and batched-product layouts
+// checked against a double-precision host product.
+//
+// Usage: test_hip_runtime            run every test (needs a GPU)
+//        test_hip_runtime --no-device  only check that hip::init() reports
+//                                      a missing GPU as std::runtime_error
+#include "harness.h"
+
+#include "RTensor/infer_shape.h"
+#include "my_hip/runtime.h"
+#include "optimiser/AdamW.h"
+
+#include <cmath>
+#include <cstring>
+#include <initializer_list>
+#include <numeric>
+#include <random>
+#include <span>
+#include <stdexcept>
+#include <vector>
+
+using Tensor = RTensor<hip::HIP, hip::kernel_type>;
+using IndexTensor = RTensor<hip::HIP, hip::index_type>;
+
+namespace {
+
+constexpr float EPS = 1e-5f; // the reference tests' absolute tolerance
+
+void fill(Tensor &t, std::initializer_list<float> values) {
+  CHECK(values.size() == t.numel());
+  t.set(std::span<const float>(values.begin(), values.size()));
+}
+
+template <typename T> std::vector<T> host(const RTensor<hip::HIP, T> &t) {
+  std::vector<T> out(t.numel());
+  t.read(std::span<T>(out));
+  return out;
+}
+
+void expect(const Tensor &t, std::initializer_list<float> values, float tol = EPS) {
+  const auto got = host(t);
+  CHECK(got.size() == values.size());
+  size_t i = 0;
+  for (float v : values) {
+    if (i < got.size()) CHECK_NEAR(got[i], v, tol);
+    ++i;
+  }
+}
+
+void expect_shape(const Tensor &t, std::initializer_list<uint32_t> shape) {
+  CHECK(t.shape() == std::vector<uint32_t>(shape));
+}
+
+// One start/submit/wait bracket around `body`, aborting on exceptions
+// (the pattern of passes::Compiled, include/passes/compile.h:174-184).
+template <typename F> void run(hip::Runtime &rt, F &&body) {
+  rt.start();
+  try {
+    body();
+    rt.submit();
+    rt.wait();
+  } catch (...) {
+    rt.abort();
+    throw;
+  }
+}
+
+std::vector<float> random_values(size_t n, uint32_t seed) {
+  std::mt19937 gen(seed);
+  std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+  std::vector<float> v(n);
+  for (auto &x : v) x = dist(gen);
+  return v;
+}
+
+// ---- the reference's known-answer tests ------------------------------------
+
+void lifecycle(hip::Runtime &rt) { // test_metal_runtime.cpp:83-123
+  CHECK_THROWS(std::logic_error, rt.submit());
+  rt.start();
+  CHECK_THROWS(std::logic_error, rt.start());
+  rt.abort();
+  rt.start();
+  rt.submit();
+  CHECK_THROWS(std::logic_error, rt.submit());
+  rt.wait();
+  CHECK_THROWS(std::logic_error, rt.wait());
+}
+
+void binary_and_chained(hip::Runtime &rt) { // 131-158
+  Tensor a({2, 2}), b({2, 2});
+  fill(a, {1, 2, 3, 4});
+  fill(b, {5, 6, 7, 8});
+  Tensor added({2, 2}), subtracted({2, 2}), multiplied({2, 2}), divided({2, 2}), chained({2, 2});
+  run(rt, [&] {
+    rt.add(a, b, added);
+    rt.sub(a, b, subtracted);
+    rt.hadamard(a, b, multiplied);
+    rt.divide(a, b, divided);
+    rt.hadamard(added, a, chained);
+  });
+  expect(added, {6, 8, 10, 12});
+  expect(subtracted, {-4, -4, -4, -4});
+  expect(multiplied, {5, 12, 21, 32});
+  expect(divided, {0.2f, 1.0f / 3.0f, 3.0f / 7.0f, 0.5f});
+  expect(chained, {6, 16, 30, 48});
+}
+
+void broadcasting(hip::Runtime &rt) { // 160-174
+  Tensor m({2, 3}), row({3}), out({2, 3});
+  fill(m, {1, 2, 3, 4, 5, 6});
+  fill(row, {10, 20, 30});
+  run(rt, [&] { rt.add(m, row, out); });
+  expect_shape(out, {2, 3});
+  expect(out, {11, 22, 33, 14, 25, 36});
+}
+
+void scalar_ops(hip::Runtime &rt) { // 176-199
+  Tensor in({2, 2}), added({2, 2}), divided({2, 2}), cubed({2, 2}), in_place({2, 2});
+  fill(in, {2, 4, 6, 8});
+  fill(in_place, {2, 4, 6, 8});
+  run(rt, [&] {
+    rt.add(in, 3.0f, added);
+    rt.divide(in, 2.0f, divided);
+    rt.pow(in, 3.0f, cubed);
+    rt.divide(in_place, 2.0f, in_place);
+    rt.pow(in_place, 2.0f, in_place);
+  });
+  expect(added, {5, 7, 9, 11});
+  expect(divided, {1, 2, 3, 4});
+  expect(cubed, {8, 64, 216, 512}, 1e-3f);
+  expect(in_place, {1, 4, 9, 16}, 1e-3f);
+}
+
+void unary_ops(hip::Runtime &rt) { // 201-226
+  Tensor in({4}), squares({4}), sig({4}), ex({4}), root({4});
+  fill(in, {0, 1, -1, 2});
+  fill(squares, {0, 1, 4, 9});
+  run(rt, [&] {
+    rt.sigmoid(in, sig);
+    rt.exp(in, ex);
+    rt.sqrt(squares, root);
+  });
+  expect(sig, {0.5f, 1.0f / (1.0f + std::exp(-1.0f)), 1.0f / (1.0f + std::exp(1.0f)),
+               1.0f / (1.0f + std::exp(-2.0f))});
+  expect(ex, {1.0f, std::exp(1.0f), std::exp(-1.0f), std::exp(2.0f)});
+  expect(root, {0, 1, 2, 3});
+}
+
+void rms_and_rms_norm(hip::Runtime &rt) { // 228-244
+  Tensor in({2, 2}), rms({2, 1}), norm({2, 2});
+  fill(in, {3, 4, 0, 0});
+  run(rt, [&] {
+    rt.RMS(in, rms);
+    rt.RMSNorm(in, norm);
+  });
+  const float r = std::sqrt(12.5f + 1e-6f);
+  expect(rms, {r, 1e-3f}); // a zero row has rms sqrt(eps) = 1e-3
+  expect(norm, {3.0f / r, 4.0f / r, 0, 0});
+}
+
+void gelu(hip::Runtime &rt) { // 246-279
+  Tensor in({5}), out({5}), der({5});
+  fill(in, {-2, -1, 0, 1, 2});
+  run(rt, [&] {
+    rt.GELU(in, out);
+    rt.GELU_derivative(in, der);
+  });
+  const auto f = [](float x) {
+    return 0.5f * x * (1.0f + std::tanh(0.7978845608f * (x + 0.044715f * x * x * x)));
+  };
+  const auto df = [](float x) {
+    const float a = 0.7978845608f, b = 0.044715f, t = std::tanh(a * (x + b * x * x * x));
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * a * (1.0f + 3.0f * b * x * x);
+  };
+  expect(out, {f(-2), f(-1), f(0), f(1), f(2)});
+  expect(der, {df(-2), df(-1), df(0), df(1), df(2)});
+}
+
+void matmul(hip::Runtime &rt) { // 281-305
+  Tensor a({2, 3}), b({3, 2}), ba({2, 2, 2}), bb({2, 2, 2}), out({2, 2}), bout({2, 2, 2});
+  fill(a, {1, 2, 3, 4, 5, 6});
+  fill(b, {7, 8, 9, 10, 11, 12});
+  fill(ba, {1, 2, 3, 4, 2, 0, 1, 2});
+  fill(bb, {5, 6, 7, 8, 1, 3, 4, 2});
+  run(rt, [&] {
+    rt.mult(a, b, out);
+    rt.mult(ba, bb, bout);
+  });
+  expect(out, {58, 64, 139, 154});
+  expect(bout, {19, 22, 43, 50, 2, 6, 9, 7});
+}
+
+void tiled_identity_matmul(hip::Runtime &rt) { // 307-342
+  constexpr uint32_t n = 64, batches = 2;
+  Tensor id({batches, n, n}), vals({batches, n, n}), out({batches, n, n});
+  std::vector<float> idv(batches * n * n, 0.0f), v(batches * n * n);
+  for (uint32_t b = 0; b < batches; ++b)
+    for (uint32_t r = 0; r < n; ++r) idv[b * n * n + r * n + r] = 1.0f;
+  for (uint32_t i = 0; i < v.size(); ++i) v[i] = float(i % 31) - 15.0f;
+  id.set(idv);
+  vals.set(v);
+  run(rt, [&] { rt.mult(id, vals, out); });
+  const auto got = host(out);
+  size_t bad = 0;
+  for (size_t i = 0; i < got.size(); ++i) bad += std::fabs(got[i] - v[i]) >= EPS;
+  CHECK(bad == 0);
+}
+
+void reductions_and_transpose(hip::Runtime &rt) { // 344-374
+  Tensor in({2, 3});
+  fill(in, {1, 2, 3, 4, 5, 6});
+  const std::vector<uint32_t> col = {2, 1}, row = {1, 3};
+  Tensor total({1}), row_sums({2, 1}), col_sums(row), row_max(col), tr({3, 2});
+  run(rt, [&] {
+    rt.sum(in, total);
+    rt.sum(in, 1, row_sums);
+    rt.sum_to_shape(in, row, col_sums);
+    rt.max_to_shape(in, col, row_max);
+    rt.transpose(in, tr);
+  });
+  expect(total, {21});
+  expect(row_sums, {6, 15});
+  expect(col_sums, {5, 7, 9});
+  expect(row_max, {3, 6});
+  expect_shape(tr, {3, 2});
+  expect(tr, {1, 4, 2, 5, 3, 6});
+}
+
+void sum_to_shape_multi(hip::Runtime &rt) { // 376-413
+  Tensor in({2, 3, 4});
+  std::vector<float> v(24);
+  std::iota(v.begin(), v.end(), 1.0f);
+  in.set(v);
+  const std::vector<uint32_t> s1 = {1, 3, 1}, s2 = {2, 1, 1}, s3 = {1, 1, 1}, s4 = {4};
+  Tensor o1(s1), o2(s2), o3(s3), o4(s4);
+  run(rt, [&] {
+    rt.sum_to_shape(in, s1, o1);
+    rt.sum_to_shape(in, s2, o2);
+    rt.sum_to_shape(in, s3, o3);
+    rt.sum_to_shape(in, s4, o4);
+  });
+  expect(o1, {68, 100, 132});
+  expect(o2, {78, 222});
+  expect(o3, {300});
+  expect(o4, {66, 72, 78, 84});
+}
+
+void sum_to_shape_leading_singletons(hip::Runtime &rt) { // 415-430
+  Tensor in({1, 4});
+  fill(in, {1, 2, 3, 4});
+  const std::vector<uint32_t> s = {4};
+  Tensor out(s);
+  run(rt, [&] { rt.sum_to_shape(in, s, out); });
+  expect_shape(out, {4});
+  expect(out, {1, 2, 3, 4});
+}
+
+void softmax(hip::Runtime &rt) { // 432-472
+  Tensor in({2, 3}), out({2, 3}), r1({3}), r1o({3}), r4({2, 2, 1, 3}), r4o({2, 2, 1, 3}),
+      single({2, 1}), singleo({2, 1});
+  fill(in, {1, 2, 3, 1, 1, 1});
+  fill(r1, {1, 2, 3});
+  fill(r4, {1, 2, 3, 3, 2, 1, 1000, 1001, 1002, -1000, -1000, -1000});
+  fill(single, {4, -7});
+  run(rt, [&] {
+    rt.softmax(in, out);
+    rt.softmax(r1, r1o);
+    rt.softmax(r4, r4o);
+    rt.softmax(single, singleo);
+  });
+  const float d = std::exp(-2.0f) + std::exp(-1.0f) + 1.0f;
+  const float lo = std::exp(-2.0f) / d, mid = std::exp(-1.0f) / d, hi = 1.0f / d, t = 1.0f / 3.0f;
+  expect(out, {lo, mid, hi, t, t, t});
+  expect(r1o, {lo, mid, hi});
+  expect(r4o, {lo, mid, hi, hi, mid, lo, lo, mid, hi, t, t, t});
+  expect(singleo, {1, 1});
+}
+
+void cross_entropy(hip::Runtime &rt) { // 474-507
+  Tensor logits({2, 2, 3}), losses({2, 2, 1}), grads({2, 2, 3});
+  fill(logits, {1, 2, 3, 1, 1, 1, 1000, 1001, 1002, -1, -2, -3});
+  IndexTensor targets({2, 2});
+  const std::vector<uint32_t> tv = {2, 0, 1, 2};
+  targets.set(tv);
+  run(rt, [&] {
+    rt.cross_entropy(logits, targets, losses);
+    rt.cross_entropy_derivative(logits, targets, grads);
+  });
+  const float d = std::exp(-2.0f) + std::exp(-1.0f) + 1.0f;
+  const float lo = std::exp(-2.0f) / d, mid = std::exp(-1.0f) / d, hi = 1.0f / d, ld = std::log(d);
+  expect(losses, {ld, std::log(3.0f), 1.0f + ld, 2.0f + ld}, 1e-4f);
+  expect(grads, {lo, mid, hi - 1.0f, -2.0f / 3.0f, 1.0f / 3.0f, 1.0f / 3.0f, lo, mid - 1.0f, hi, hi,
+                 mid, lo - 1.0f},
+         1e-4f);
+}
+
+void cross_entropy_bad_target(hip::Runtime &rt) {
+  // A target outside the vocabulary gives +INF loss and a row of +INF
+  // gradients (math.metal:893-896, 921-926).
+  Tensor logits({2, 3}), loss({2, 1}), grad({2, 3});
+  fill(logits, {1, 2, 3, 4, 5, 6});
+  IndexTensor targets({2});
+  const std::vector<uint32_t> tv = {1, 3};
+  targets.set(tv);
+  run(rt, [&] {
+    rt.cross_entropy(logits, targets, loss);
+    rt.cross_entropy_derivative(logits, targets, grad);
+  });
+  const auto l = host(loss), g = host(grad);
+  CHECK(std::isfinite(l[0]));
+  CHECK(std::isinf(l[1]) && l[1] > 0);
+  for (int i = 3; i < 6; ++i) CHECK(std::isinf(g[i]) && g[i] > 0);
+}
+
+void argmax(hip::Runtime &rt) { // 509-531
+  Tensor small({2, 3});
+  fill(small, {1, 4, 2, 9, 3, 5});
+  Tensor large({5000});
+  std::vector<float> v(5000, 0.0f);
+  v[4097] = 100.0f;
+  large.set(v);
+  Tensor ties({6});
+  fill(ties, {1, 7, 7, 2, 7, 0}); // lowest index of the maximum wins
+  IndexTensor so({1, 1}), lo({1, 1}), to({1, 1});
+  run(rt, [&] {
+    rt.argmax(small, so);
+    rt.argmax(large, lo);
+    rt.argmax(ties, to);
+  });
+  CHECK(host(so)[0] == 3);
+  CHECK(host(lo)[0] == 4097);
+  CHECK(host(to)[0] == 1);
+}
+
+void embedding_lookup(hip::Runtime &rt) { // 533-549
+  Tensor w({4, 3}), out({2, 2, 3});
+  fill(w, {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12});
+  IndexTensor ids({2, 2});
+  const std::vector<uint32_t> iv = {2, 0, 3, 1};
+  ids.set(iv);
+  run(rt, [&] { rt.embedding_lookup(w, ids, out); });
+  expect(out, {7, 8, 9, 1, 2, 3, 10, 11, 12, 4, 5, 6}, 0.0f);
+}
+
+void scatter_index(hip::Runtime &rt) { // 551-569
+  Tensor values({2, 2, 3}), out({4, 3});
+  fill(values, {1, 2, 3, 4, 5, 6, 10, 20, 30, 7, 8, 9});
+  IndexTensor ids({2, 2});
+  const std::vector<uint32_t> iv = {2, 0, 2, 1};
+  ids.set(iv);
+  fill(out, {99, 99, 99, 99, 99, 99, 99, 99, 99, 99, 99, 99});
+  run(rt, [&] { rt.scatter_index(values, ids, out); });
+  expect(out, {4, 5, 6, 7, 8, 9, 11, 22, 33, 0, 0, 0});
+}
+
+void scatter_add_rows(hip::Runtime &rt) { // 571-593
+  Tensor base({4, 3}), values({2, 2, 3}), out({4, 3});
+  fill(base, {100, 101, 102, 103, 104, 105, 106, 107, 108, 109, 110, 111});
+  fill(values, {1, 2, 3, 4, 5, 6, 10, 20, 30, 7, 8, 9});
+  IndexTensor ids({2, 2});
+  const std::vector<uint32_t> iv = {2, 0, 2, 1};
+  ids.set(iv);
+  run(rt, [&] { rt.scatter_add_rows(base, ids, values, out); });
+  expect(out, {104, 106, 108, 110, 112, 114, 117, 129, 141, 109, 110, 111});
+  expect(base, {100, 101, 102, 103, 104, 105, 106, 107, 108, 109, 110, 111}); // base untouched
+}
+
+void gradient_clipping(hip::Runtime &rt) { // 595-615
+  Tensor first({3}), second({1});
+  Tensor s = Tensor::from_zeros({1});
+  fill(first, {3, 4, 0});
+  fill(second, {12});
+  run(rt, [&] {
+    rt.accumulate_gradient_squared_norm(first, s);
+    rt.accumulate_gradient_squared_norm(second, s);
+    rt.clip_gradient(first, s, 1.0f, first);
+    rt.clip_gradient(second, s, 1.0f, second);
+  });
+  expect(s, {169});
+  expect(first, {3.0f / 13, 4.0f / 13, 0});
+  expect(second, {12.0f / 13});
+}
+
+void adamw(hip::Runtime &rt) { // 617-658
+  using AdamW = Optimiser::AdamW<Tensor>;
+  Tensor p({4}), g({4});
+  fill(p, {1, -2, 3, -4});
+  fill(g, {0.5f, -0.25f, 1.0f, -0.75f});
+  AdamW opt;
+  auto params = AdamW::generate_params(0.01f, 0.9f, 0.999f, 1e-8f, 0.01f);
+  std::vector<float> e = {1, -2, 3, -4}, m1(4, 0.0f), m2(4, 0.0f);
+  const std::vector<float> gv = {0.5f, -0.25f, 1.0f, -0.75f};
+  for (uint32_t step = 1; step <= 2; ++step) {
+    run(rt, [&] { opt.update(rt, params, p, g, p); });
+    const float c1 = 1.0f - std::pow(0.9f, float(step)), c2 = 1.0f - std::pow(0.999f, float(step));
+    for (size_t i = 0; i < 4; ++i) {
+      m1[i] = 0.9f * m1[i] + 0.1f * gv[i];
+      m2[i] = 0.999f * m2[i] + 0.001f * gv[i] * gv[i];
+      e[i] = e[i] * 0.9999f - 0.01f * (m1[i] / c1) / (std::sqrt(m2[i] / c2) + 1e-8f);
+    }
+    expect(p, {e[0], e[1], e[2], e[3]}, 1e-5f);
+  }
+  CHECK(opt.step() == 2);
+}
+
+void cleanup_is_idempotent() { // 125-129
+  hip::Runtime rt;
+  rt.cleanup();
+  rt.cleanup();
+}
+
+// ---- validation the executor relies on ----------------------------------------
+
+void validation(hip::Runtime &rt) {
+  Tensor a({2, 3}), b({3, 2}), wrong({3, 3}), ok({2, 2});
+  // ops outside start..submit
+  CHECK_THROWS(std::logic_error, rt.add(a, a, a));
+  rt.start();
+  CHECK_THROWS(std::invalid_argument, rt.mult(a, b, wrong));
+  CHECK_THROWS(std::invalid_argument, rt.mult(a, a, ok)); // inner dims differ
+  CHECK_THROWS(std::runtime_error, rt.add(a, b, a));       // cannot broadcast
+  CHECK_THROWS(std::invalid_argument, rt.add(a, 1.0f, wrong));
+  CHECK_THROWS(std::invalid_argument, rt.transpose(a, a));
+  CHECK_THROWS(std::out_of_range, rt.transpose(a, b, 0, 2));
+  CHECK_THROWS(std::out_of_range, rt.sum(a, 2, ok));
+  CHECK_THROWS(std::invalid_argument, rt.softmax(a, b));
+  Tensor g({4}), p({4}), m({4}), v({4}), s1({1}), bad({2});
+  CHECK_THROWS(std::invalid_argument, rt.adamW(p, g, p, m, v, s1, s1, s1, s1, 1e-8f, 0));
+  CHECK_THROWS(std::invalid_argument, rt.adamW(p, g, p, m, v, bad, s1, s1, s1, 1e-8f, 1));
+  CHECK_THROWS(std::invalid_argument, rt.clip_gradient(g, s1, 0.0f, g));
+  CHECK_THROWS(std::invalid_argument, rt.clip_gradient(g, s1, NAN, g));
+  Tensor w({4, 3}), emb_bad({2, 3});
+  IndexTensor ids({2, 2});
+  CHECK_THROWS(std::invalid_argument, rt.embedding_lookup(w, ids, emb_bad));
+  Tensor logits({2, 3}), loss_bad({2});
+  IndexTensor targets({2});
+  CHECK_THROWS(std::invalid_argument, rt.cross_entropy(logits, targets, loss_bad));
+  Tensor r({2, 3}), rms_bad({2, 3});
+  CHECK_THROWS(std::invalid_argument, rt.RMS(r, rms_bad));
+  const std::vector<uint32_t> two_shrinks = {1, 1};
+  Tensor mx({1, 1});
+  CHECK_THROWS(std::invalid_argument, rt.max_to_shape(a, two_shrinks, mx));
+  rt.abort();
+}
+
+void max_to_shape_alias(hip::Runtime &rt) {
+  // Nothing to shrink: the destination becomes the input (runtime.cpp:629-632).
+  Tensor a({2, 3}), out({2, 3});
+  fill(a, {1, 2, 3, 4, 5, 6});
+  const std::vector<uint32_t> same = {2, 3};
+  run(rt, [&] { rt.max_to_shape(a, same, out); });
+  CHECK(out.get_storage() == a.get_storage());
+  CHECK(a.get_storage()->ref_count == 2);
+}
+
+void in_place_and_split_merge(hip::Runtime &rt) {
+  Tensor x({2, 4}), bias({1, 4}), split({2, 2, 2}), merged({2, 4});
+  fill(x, {1, 2, 3, 4, 5, 6, 7, 8});
+  fill(bias, {10, 20, 30, 40});
+  run(rt, [&] {
+    rt.add(x, bias, x); // the executor's LINEAR bias add (execute.h:249)
+    rt.split_last_dim(x, split, 2, 2);
+    rt.merge_last_dims(split, merged, 2, 2);
+  });
+  expect(x, {11, 22, 33, 44, 15, 26, 37, 48});
+  expect(split, {11, 22, 33, 44, 15, 26, 37, 48});
+  expect(merged, {11, 22, 33, 44, 15, 26, 37, 48});
+  CHECK(split.get_storage() != x.get_storage());
+}
+
+// Double-precision host product for the batched layouts of the GPT:
+// weight broadcast [B,T,D].[D,F], attention [B,H,T,d].[B,H,d,T] and a rank-3
+// by rank-4 broadcast of the batch dims.
+void batched_matmul_layouts(hip::Runtime &rt) {
+  struct Case {
+    std::vector<uint32_t> a, b;
+  };
+  const Case cases[] = {{{4, 24, 32}, {32, 40}},
+                        {{2, 3, 17, 64}, {2, 3, 64, 19}},
+                        {{3, 1, 8, 16}, {1, 2, 16, 8}},
+                        {{5, 33, 7}, {5, 7, 65}}};
+  uint32_t seed = 1;
+  for (const Case &c : cases) {
+    const auto shape = rtensor::infer_mult(c.a, c.b);
+    Tensor a(c.a), b(c.b), out(shape);
+    const auto av = random_values(a.numel(), seed++), bv = random_values(b.numel(), seed++);
+    a.set(av);
+    b.set(bv);
+    run(rt, [&] { rt.mult(a, b, out); });
+    const auto got = host(out);
+    const size_t r = shape.size();
+    const uint32_t M = shape[r - 2], N = shape[r - 1], K = c.a.back();
+    // decode each output batch index into the operands' broadcast offsets
+    const size_t batches = out.numel() / (size_t(M) * N);
+    double max_err = 0, max_ref = 0;
+    for (size_t bi = 0; bi < batches; ++bi) {
+      size_t rem = bi, off_a = 0, off_b = 0, sa = 1, sb = 1;
+      for (size_t d = r - 2; d-- > 0;) {
+        const uint32_t dim = shape[d];
+        const uint32_t idx = uint32_t(rem % dim);
+        rem /= dim;
+        const size_t da = d + c.a.size() >= r ? d + c.a.size() - r : size_t(-1);
+        const size_t db = d + c.b.size() >= r ? d + c.b.size() - r : size_t(-1);
+        if (da != size_t(-1)) {
+          if (c.a[da] != 1) off_a += idx * sa;
+          sa *= c.a[da];
+        }
+        if (db != size_t(-1)) {
+          if (c.b[db] != 1) off_b += idx * sb;
+          sb *= c.b[db];
+        }
+      }
+      for (uint32_t m = 0; m < M; ++m)
+        for (uint32_t n = 0; n < N; ++n) {
+          double acc = 0;
+          for (uint32_t k = 0; k < K; ++k)
+            acc += double(av[off_a * M * K + m * K + k]) * bv[off_b * K * N + k * N + n];
+          max_err = std::max(max_err, std::fabs(acc - got[bi * M * N + m * N + n]));
+          max_ref = std::max(max_ref, std::fabs(acc));
+        }
+    }
+    CHECK(max_err <= 1e-3 * max_ref); // matmul tolerance: rel 1e-3
+  }
+}
+
+// Graph mode: the same recording replayed from the cache gives the eager
+// result, and a repeat refreshes the cached graph instead of rebuilding it.
+void graph_mode(hip::Runtime &rt) {
+  Tensor x({64, 96}), w({96, 128}), bias({1, 128}), y({64, 128}), z({64, 128});
+  x.set(random_values(x.numel(), 11));
+  w.set(random_values(w.numel(), 12));
+  bias.set(random_values(bias.numel(), 13));
+  const auto step = [&] {
+    Tensor tmp({64, 128}); // a per-call temporary like the executor's
+    rt.mult(x, w, tmp);
+    rt.add(tmp, bias, tmp);
+    rt.GELU(tmp, y);
+    rt.softmax(y, z);
+  };
+  run(rt, step);
+  const auto eager = host(z);
+  rt.set_graph_mode(true);
+  for (int i = 0; i < 3; ++i) {
+    z.get_storage()->fill(0.0f);
+    run(rt, step);
+    const auto got = host(z);
+    double err = 0;
+    for (size_t k = 0; k < got.size(); ++k) err = std::max(err, double(std::fabs(got[k] - eager[k])));
+    CHECK(err == 0.0);
+  }
+  const auto stats = rt.graph_stats();
+  CHECK(stats.captures == 3);
+  CHECK(stats.instantiations == 1);
+  CHECK(stats.updates == 2);
+  // Host writes while recording land at record time (EXPR_CONSTANT,
+  // include/passes/execute.h:458-466).
+  Tensor c({1, 1}), out({1, 1});
+  run(rt, [&] {
+    const float v = 2.5f;
+    c.set(std::span<const float>(&v, 1));
+    rt.add(c, 1.0f, out);
+  });
+  expect(out, {3.5f});
+  rt.set_graph_mode(false);
+}
+
+void memory_pool_reuse(hip::Runtime &) {
+  const auto before = hip::memory_stats();
+  for (int i = 0; i < 10; ++i) {
+    Tensor t({256, 1024});
+    t.get_storage()->fill(1.0f);
+  }
+  const auto after = hip::memory_stats();
+  CHECK(after.device_allocations - before.device_allocations <= 1);
+  CHECK(after.in_use_bytes == before.in_use_bytes);
+}
+
+void storage_semantics(hip::Runtime &) {
+  Tensor a = Tensor::from_values({{1, 2}, {3, 4}});
+  Tensor b = a.clone();
+  CHECK(a == b);
+  b.set(9.0f, 1, 1);
+  CHECK(!(a == b));
+  CHECK(b.get(1, 1) == 9.0f);
+  CHECK(a.get(1, 0) == 3.0f);
+  std::vector<float> big(4);
+  CHECK_THROWS(std::out_of_range, a.get_storage()->read(std::span<float>(big.data(), 3), 2));
+  const std::vector<uint32_t> flat = {4};
+  Tensor v = a.view(flat);
+  CHECK(v.get_storage() == a.get_storage());
+  CHECK(a.get_storage()->ref_count == 2);
+  Tensor z = Tensor::from_zeros({3, 5});
+  for (float x : host(z)) CHECK(x == 0.0f);
+}
+
+} // namespace
+
+int main(int argc, char **argv) {
+  if (argc > 1 && std::strcmp(argv[1], "--no-device") == 0) {
+    harness::run("init_without_device_throws", [] {
+      CHECK_THROWS(std::runtime_error, hip::init(0));
+      CHECK(!hip::initialised());
+      CHECK_THROWS(std::logic_error, hip::Runtime());
+    });
+    return harness::failures();
+  }
+  hip::init(0);
+  {
+    hip::Runtime rt;
+    harness::run("lifecycle", [&] { lifecycle(rt); });
+    harness::run("binary_and_chained_operations", [&] { binary_and_chained(rt); });
+    harness::run("broadcasting", [&] { broadcasting(rt); });
+    harness::run("scalar_operations", [&] { scalar_ops(rt); });
+    harness::run("unary_operations", [&] { unary_ops(rt); });
+    harness::run("rms_and_rms_norm", [&] { rms_and_rms_norm(rt); });
+    harness::run("gelu", [&] { gelu(rt); });
+    harness::run("matmul", [&] { matmul(rt); });
+    harness::run("tiled_identity_matmul", [&] { tiled_identity_matmul(rt); });
+    harness::run("reductions_and_transpose", [&] { reductions_and_transpose(rt); });
+    harness::run("sum_to_shape_multiple_dimensions", [&] { sum_to_shape_multi(rt); });
+    harness::run("sum_to_shape_leading_singletons", [&] { sum_to_shape_leading_singletons(rt); });
+    harness::run("softmax", [&] { softmax(rt); });
+    harness::run("cross_entropy", [&] { cross_entropy(rt); });
+    harness::run("cross_entropy_bad_target", [&] { cross_entropy_bad_target(rt); });
+    harness::run("argmax", [&] { argmax(rt); });
+    harness::run("embedding_lookup", [&] { embedding_lookup(rt); });
+    harness::run("scatter_index", [&] { scatter_index(rt); });
+    harness::run("scatter_add_rows", [&] { scatter_add_rows(rt); });
+    harness::run("gradient_clipping", [&] { gradient_clipping(rt); });
+    harness::run("adamw", [&] { adamw(rt); });
+    harness::run("validation", [&] { validation(rt); });
+    harness::run("max_to_shape_alias", [&] { max_to_shape_alias(rt); });
+    harness::run("in_place_and_split_merge", [&] { in_place_and_split_merge(rt); });
+    harness::run("batched_matmul_layouts", [&] { batched_matmul_layouts(rt); });
+    harness::run("graph_mode", [&] { graph_mode(rt); });
+    harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
+    harness::run("storage_semantics", [&] { storage_semantics(rt); });
+  }
+  harness::run("cleanup_is_idempotent", cleanup_is_idempotent);
+  hip::shutdown();
+  std::printf("%s\n", harness::failures() ? "SOME TESTS FAILED" : "all hip::Runtime tests passed");
+  return harness::failures();
+}

@@ -443,9 +443,29 @@ def test_embedding_add_positions(g):
     tok, pos = O.normal((V, D), 65), O.normal((T, D), 66)
     ids = O.uniform_u32((B, T), 67, V)
     out = g.empty((B, T, D))
-    g.call("tlh_embedding_add_positions", g.dev(tok), g.dev(pos), g.dev(ids), B, T, D, out)
+    g.call("tlh_embedding_add_positions", g.dev(tok), V, g.dev(pos), g.dev(ids), B, T, D, out)
     expect = O.embedding_lookup(tok, ids) + pos[None, :, :]
     np.testing.assert_array_equal(g.host(out), expect)
+
+
+def test_embedding_out_of_range_ids(g):
+    # The reference reads unchecked; an id past the table gives a NaN row
+    # (gather) or is dropped (scatter), never an access outside the table.
+    rows, dim = 5, 8
+    w = O.normal((rows, dim), 70)
+    ids = np.array([1, 5, 0, 1000000], np.uint32)
+    out = g.empty((4, dim))
+    g.call("tlh_embedding_lookup", g.dev(w), rows, dim, g.dev(ids), 4, out)
+    got = g.host(out)
+    np.testing.assert_array_equal(got[[0, 2]], w[[1, 0]])
+    assert np.isnan(got[[1, 3]]).all()
+    dst = g.zeros((rows, dim))
+    values = O.normal((4, dim), 71)
+    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), 4, dim, dst, rows)
+    expect = np.zeros((rows, dim), np.float32)
+    expect[1] += values[0]
+    expect[0] += values[2]
+    np.testing.assert_array_equal(g.host(dst), expect)
 
 
 def test_scatter_add_rows(g):
@@ -454,13 +474,13 @@ def test_scatter_add_rows(g):
     values = np.array([1, 2, 3, 4, 5, 6, 10, 20, 30, 7, 8, 9], np.float32).reshape(4, 3)
     ids = np.array([2, 0, 2, 1], np.uint32)
     dst = g.dev(base)
-    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), 4, 3, dst)
+    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), 4, 3, dst, 4)
     np.testing.assert_allclose(g.host(dst), O.scatter_add_rows(base, ids, values), atol=1e-4)
     V, D, n = 2048, 384, 6144
     values = O.normal((n, D), 68)
     ids = O.uniform_u32((n,), 69, V)
     dst = g.zeros((V, D))
-    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), n, D, dst)
+    g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), n, D, dst, V)
     assert_close(g.host(dst), O.scatter_add_rows(np.zeros((V, D), np.float32), ids, values),
                  rtol=1e-4, atol=1e-5)
 
