@@ -1,0 +1,43 @@
+"""The reference's own executor -- passes::Compiled over nn::GPT (4 decoder
+blocks), AdamW, clip 1.0, src/train.cpp's loop body -- driving hip::Runtime.
+
+oracle/_ref/dropin_gpt is built by oracle/Makefile (target `dropin`) from
+the reference headers where they lie, with hip::Runtime compiled in
+unchanged; see oracle/dropin_gpt.cpp. It compares two training steps on
+hip::Runtime (eager and graph mode) with the same program on the CPU
+oracle runtime, and the oracle runtime with the oracle's hand-derived GPT
+step (weights identified by value).
+"""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+BIN = ROOT / "oracle" / "_ref" / "dropin_gpt"
+
+needs_bin = pytest.mark.skipif(
+    not BIN.exists(),
+    reason="oracle/_ref/dropin_gpt not built (needs the reference tree: make -C oracle dropin)")
+
+
+def _run(*args, timeout=300):
+    proc = subprocess.run([str(BIN), *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                          text=True, timeout=timeout)
+    print(proc.stdout)
+    return proc
+
+
+@needs_bin
+def test_reference_executor_on_oracle_runtime_matches_oracle_gpt():
+    proc = _run("--cpu-only")
+    assert proc.returncode == 0, proc.stdout
+    assert "oracle anchor ok" in proc.stdout
+
+
+@needs_bin
+@pytest.mark.gpu
+def test_reference_executor_on_hip_runtime():
+    proc = _run()
+    assert proc.returncode == 0, proc.stdout
+    assert "drop-in parity ok" in proc.stdout
