@@ -222,6 +222,12 @@ typedef struct tlh_gemm_desc {
 int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
 /* fp32 elements of workspace tlh_gemm wants for `desc` (0: none needed). */
 int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
+/* Tuning hook: force every following tlh_gemm / tlh_matmul to use a
+ * bm x bn tile (64 or 128 each), a K tile of bk (16 or 32) and, where a
+ * workspace allows it, `splits` K splits; bm = bn = 0 restores the
+ * automatic plan. Process-wide, for measurement sweeps. A forced split
+ * count needs a workspace sized for it (tlh_gemm_workspace_size). */
+int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------
  * Reductions (math.metal:549-564, 618-777, 955-983)

@@ -23,7 +23,7 @@
 namespace tlh {
 namespace {
 
-constexpr int kBK = 16;
+constexpr int kBK = 32; // largest K tile; split-K chunks are multiples of it
 constexpr int kPad = 4;
 
 struct GemmParams {
@@ -74,9 +74,11 @@ __device__ inline void epilogue_store(const GemmParams &p, float *C, int m, int 
   C[idx] = v;
 }
 
-template <int BM, int BN, int WM, int WN, bool TA, bool TB, bool VEC>
+// FULL: M, N are multiples of the tile, the K range of every block is a
+// multiple of BK and the operands are float4-aligned: no bounds checks.
+template <int BM, int BN, int WM, int WN, int BK, bool TA, bool TB, bool VEC, bool FULL>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
-  constexpr int BK = kBK;
+  static_assert(BK % 8 == 0 && BK <= kBK, "K tile must be a multiple of 8 and divide the split chunk");
   constexpr int TM = WM / 32;
   constexpr int TN = WN / 32;
   constexpr int WAVES_N = BN / WN;
@@ -145,17 +147,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int row_lim = TA ? k_end : p.M;
       const int col_lim = TA ? p.M : k_end;
       const float *src = A + size_t(grow) * p.lda + gcol;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (grow < row_lim) {
-        if (VEC && gcol + 3 < col_lim) {
-          v = *reinterpret_cast<const f4 *>(src);
-        } else {
+      if constexpr (FULL) {
+        ra[i] = *reinterpret_cast<const f4 *>(src);
+      } else {
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (grow < row_lim) {
+          if (VEC && gcol + 3 < col_lim) {
+            v = *reinterpret_cast<const f4 *>(src);
+          } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (gcol + j < col_lim) v[j] = src[j];
+            for (int j = 0; j < 4; ++j)
+              if (gcol + j < col_lim) v[j] = src[j];
+          }
         }
+        ra[i] = v;
       }
-      ra[i] = v;
     }
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i) {
@@ -168,17 +174,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int row_lim = TB ? p.N : k_end;
       const int col_lim = TB ? k_end : p.N;
       const float *src = B + size_t(grow) * p.ldb + gcol;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (grow < row_lim) {
-        if (VEC && gcol + 3 < col_lim) {
-          v = *reinterpret_cast<const f4 *>(src);
-        } else {
+      if constexpr (FULL) {
+        rb[i] = *reinterpret_cast<const f4 *>(src);
+      } else {
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (grow < row_lim) {
+          if (VEC && gcol + 3 < col_lim) {
+            v = *reinterpret_cast<const f4 *>(src);
+          } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (gcol + j < col_lim) v[j] = src[j];
+            for (int j = 0; j < 4; ++j)
+              if (gcol + j < col_lim) v[j] = src[j];
+          }
         }
+        rb[i] = v;
       }
-      rb[i] = v;
     }
   };
 
@@ -214,42 +224,47 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int a_row0 = wm * WM + r; // + i*32
   const int b_col0 = wn * WN + r; // + j*32
 
+  // All of a lane's fragments of one K tile are read from LDS first, then
+  // the MFMAs run back to back: the LDS latency is paid once per tile.
   auto compute_tile = [&](int buf) {
     const float *as = smem + buf * (A_TILE + B_TILE);
     const float *bs = as + A_TILE;
+    constexpr int Q = BK / 8; // float4 groups per lane per K tile
+    f4 af[TM][Q], bf[TN][Q];
 #pragma unroll
-    for (int s4 = 0; s4 < BK / 8; ++s4) {
+    for (int s4 = 0; s4 < Q; ++s4) {
       const int kb = hk * (BK / 2) + s4 * 4; // first of 4 consecutive k
-      f4 af[TM], bf[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = a_row0 + i * 32;
         if (!TA) {
-          af[i] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
+          af[i][s4] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) af[i][q] = as[(kb + q) * A_LD + m];
+          for (int q = 0; q < 4; ++q) af[i][s4][q] = as[(kb + q) * A_LD + m];
         }
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = b_col0 + j * 32;
         if (TB) {
-          bf[j] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
+          bf[j][s4] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) bf[j][q] = bs[(kb + q) * B_LD + n];
+          for (int q = 0; q < 4; ++q) bf[j][s4][q] = bs[(kb + q) * B_LD + n];
         }
       }
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < Q; ++s4)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[j][q],
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s4][q], bf[j][s4][q],
                                                              acc[i][j], 0, 0, 0);
-    }
   };
 
   // Bias gradient: the blocks of the first tile row also sum the op(B)
@@ -300,11 +315,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * WN + j * 32 + r;
-      if (n >= p.N) continue;
+      if (!FULL && n >= p.N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
-        if (m >= p.M) continue;
+        if (!FULL && m >= p.M) continue;
         if (p.splits > 1) {
           C[size_t(m) * p.N + n] = acc[i][j][v];
         } else {
@@ -337,25 +352,29 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
 }
 
 struct Plan {
-  int bm, bn, splits;
+  int bm, bn, splits, bk = 16;
 };
 
-template <int BM, int BN, int WM, int WN>
-void launch_cfg(const GemmParams &p, bool ta, bool tb, bool vec, dim3 grid,
+template <int BM, int BN, int WM, int WN, int BK>
+void launch_cfg(const GemmParams &p, bool ta, bool tb, bool vec, bool full, dim3 grid,
                 hipStream_t s) {
-#define TLH_GEMM_CASE(TA_, TB_, V_)                                              \
-  if (ta == TA_ && tb == TB_ && vec == V_) {                                     \
-    gemm_mfma_kernel<BM, BN, WM, WN, TA_, TB_, V_><<<grid, 256, 0, s>>>(p);       \
+#define TLH_GEMM_CASE(TA_, TB_, V_, F_)                                          \
+  if (ta == TA_ && tb == TB_ && vec == V_ && full == F_) {                       \
+    gemm_mfma_kernel<BM, BN, WM, WN, BK, TA_, TB_, V_, F_><<<grid, 256, 0, s>>>(p); \
     return;                                                                      \
   }
-  TLH_GEMM_CASE(false, false, true)
-  TLH_GEMM_CASE(false, true, true)
-  TLH_GEMM_CASE(true, false, true)
-  TLH_GEMM_CASE(true, true, true)
-  TLH_GEMM_CASE(false, false, false)
-  TLH_GEMM_CASE(false, true, false)
-  TLH_GEMM_CASE(true, false, false)
-  TLH_GEMM_CASE(true, true, false)
+  TLH_GEMM_CASE(false, false, true, true)
+  TLH_GEMM_CASE(false, true, true, true)
+  TLH_GEMM_CASE(true, false, true, true)
+  TLH_GEMM_CASE(true, true, true, true)
+  TLH_GEMM_CASE(false, false, true, false)
+  TLH_GEMM_CASE(false, true, true, false)
+  TLH_GEMM_CASE(true, false, true, false)
+  TLH_GEMM_CASE(true, true, true, false)
+  TLH_GEMM_CASE(false, false, false, false)
+  TLH_GEMM_CASE(false, true, false, false)
+  TLH_GEMM_CASE(true, false, false, false)
+  TLH_GEMM_CASE(true, true, false, false)
 #undef TLH_GEMM_CASE
 }
 
@@ -364,28 +383,37 @@ inline size_t tiles_for(const GemmDesc &d, int bm, int bn) {
 }
 
 constexpr int kTargetBlocks = 256; // one block per CU at least
-constexpr int kMinSplitK = 128;    // K elements per split-K chunk, at least
 
-// Largest tile that still gives every CU a block; otherwise (tall-K weight
-// gradients) the largest tile whose split-K count reaches 256 blocks with
-// K chunks of >= 128.
+// Process-wide plan override for tuning sweeps (tlh_gemm_set_plan); 0 = the
+// planner decides.
+int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
+constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
+
+// Tile plan, from measurements on MI355X of the GPT step's shapes
+// (M, N, K in {384, 1536, 2048, 6144}) and the d=1024 shapes:
+//  - 128x128 tiles (K tile 16) only when they give every CU three or more
+//    blocks; their 4 accumulators per wave win when the grid is deep;
+//  - otherwise 64x64 tiles with a K tile of 32: 2-4 co-resident blocks per
+//    CU hide the global/LDS latency a single block per CU cannot;
+//  - tall-K products (weight gradients, K = B*T) with too few output tiles
+//    split K so that about 1024 blocks run, each with K chunks of >= 256.
 Plan make_plan(const GemmDesc &d, bool allow_split) {
-  static const int cfgs[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-  const size_t batch = size_t(std::max(1, d.batch));
-  for (const auto &c : cfgs)
-    if (tiles_for(d, c[0], c[1]) * batch >= kTargetBlocks) return {c[0], c[1], 1};
-  if (allow_split && batch == 1 && d.batch_ndim == 0 && d.K >= 4 * kMinSplitK) {
-    for (const auto &c : cfgs) {
-      const size_t tiles = tiles_for(d, c[0], c[1]);
-      int splits = int((kTargetBlocks + tiles - 1) / tiles);
-      splits = std::min(std::min(splits, d.K / kMinSplitK), 64);
-      if (splits >= 2 && tiles * splits >= kTargetBlocks) return {c[0], c[1], splits};
-    }
-    const size_t tiles = tiles_for(d, 64, 64);
-    const int splits = std::max(1, std::min(d.K / kMinSplitK, 64));
-    return {64, 64, tiles < kTargetBlocks ? splits : 1};
+  if (g_force_bm > 0) {
+    const bool can_split = allow_split && d.batch <= 1 && d.batch_ndim == 0;
+    return {g_force_bm, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, g_force_bk};
   }
-  return {64, 64, 1};
+  const size_t batch = size_t(std::max(1, d.batch));
+  if (tiles_for(d, 128, 128) * batch >= 3 * size_t(kTargetBlocks)) return {128, 128, 1, 16};
+  const size_t tiles = tiles_for(d, 64, 64);
+  if (allow_split && batch == 1 && d.batch_ndim == 0 && tiles * 4 < 4 * size_t(kTargetBlocks) &&
+      d.K >= 2 * kMinSplitK) {
+    int splits = 1;
+    while (splits < 16 && tiles * size_t(splits) < 4 * size_t(kTargetBlocks) &&
+           d.K / (splits * 2) >= kMinSplitK)
+      splits *= 2;
+    if (splits >= 2) return {64, 64, splits, 32};
+  }
+  return {64, 64, 1, 32};
 }
 
 bool vec_ok(const GemmDesc &d) {
@@ -448,10 +476,21 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   const int z = p.splits > 1 ? p.splits : std::max(1, d.batch);
   dim3 grid(unsigned(tiles_m * p.tiles_n), 1, unsigned(z));
   const bool ta = d.trans_a != 0, tb = d.trans_b != 0, vec = vec_ok(d);
-  if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64>(p, ta, tb, vec, grid, s);
-  else if (plan.bm == 128 && plan.bn == 64) launch_cfg<128, 64, 64, 32>(p, ta, tb, vec, grid, s);
-  else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64>(p, ta, tb, vec, grid, s);
-  else launch_cfg<64, 64, 32, 32>(p, ta, tb, vec, grid, s);
+  // Every block's K range is a multiple of the K tile when K is and the
+  // split chunk (a multiple of kBK) is.
+  const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && d.K % plan.bk == 0 &&
+                    (p.splits <= 1 || p.k_chunk % plan.bk == 0);
+  if (plan.bk == 32) {
+    if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64, 32>(p, ta, tb, vec, full, grid, s);
+    else if (plan.bm == 128 && plan.bn == 64) launch_cfg<128, 64, 64, 32, 32>(p, ta, tb, vec, full, grid, s);
+    else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64, 32>(p, ta, tb, vec, full, grid, s);
+    else launch_cfg<64, 64, 32, 32, 32>(p, ta, tb, vec, full, grid, s);
+  } else {
+    if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64, 16>(p, ta, tb, vec, full, grid, s);
+    else if (plan.bm == 128 && plan.bn == 64) launch_cfg<128, 64, 64, 32, 16>(p, ta, tb, vec, full, grid, s);
+    else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64, 16>(p, ta, tb, vec, full, grid, s);
+    else launch_cfg<64, 64, 32, 32, 16>(p, ta, tb, vec, full, grid, s);
+  }
   int st = launch_status();
   if (st) return st;
   if (p.splits > 1) {
@@ -484,6 +523,16 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
   return d;
 }
 } // namespace
+
+TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
+  const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
+  if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32)) return int(hipErrorInvalidValue);
+  tlh::g_force_bm = bm;
+  tlh::g_force_bn = bn;
+  tlh::g_force_splits = splits;
+  tlh::g_force_bk = bk;
+  return 0;
+}
 
 TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
   if (!desc) return int(hipErrorInvalidValue);

@@ -98,6 +98,7 @@ HIP_SIGNATURES: dict[str, list] = {
                    c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P, U32P, P],
     "tlh_gemm": [POINTER(GemmDesc), P],
     "tlh_gemm_workspace_size": [POINTER(GemmDesc), POINTER(c_size_t)],
+    "tlh_gemm_set_plan": [c_int, c_int, c_int, c_int],
     # reductions
     "tlh_sum": [P, c_size_t, P, P],
     "tlh_sum_to_shape": [P, P, c_uint32, U32P, U32P, P],
