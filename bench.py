@@ -9,6 +9,11 @@ line: tokens/s, the GEMM roofline fraction (fp32 MFMA), the d=1024 GEMM
 rate, and the CPU oracle's rate on a bounded sample of the same step.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Profiling runs (rocprofv3 counters) use --eager (time eager steps, one
+dispatch per kernel instead of graph replays), --skip-d1024 and
+--copy-calibration MiB (one device copy of that size, whose FETCH_SIZE /
+WRITE_SIZE readings scale the counters to bytes).
 """
 from __future__ import annotations
 
@@ -77,6 +82,43 @@ def gemm_d1024(hip, stream) -> dict:
             hip.tlh_free(b)
 
 
+def gemm_traffic() -> float | None:
+    """HBM bytes per GEMM launch from the committed counter profile (two
+    rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, scaled by a copy of
+    known size; the file names the commands)."""
+    path = ROOT / "profiles" / "gpt_step_b32_t192_d384_gemm_hbm_traffic.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("machine-readable:"):
+                fields = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+                return float(fields["gemm_traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+    return None
+
+
+def copy_calibration(hip, stream, mib: int) -> None:
+    """One device-to-device copy of `mib` MiB (tlh_copy): its FETCH_SIZE and
+    WRITE_SIZE readings must equal the copy size, which calibrates the
+    counters of the other kernels."""
+    from templit_amd.native import check
+
+    n = mib * (1 << 20) // 4
+    bufs = []
+    for _ in range(2):
+        ptr = ctypes.c_void_p()
+        check(hip.tlh_malloc(ctypes.byref(ptr), n * 4), "malloc")
+        bufs.append(ptr.value)
+    try:
+        check(hip.tlh_fill_f32(bufs[0], 1.0, n, stream), "fill")
+        check(hip.tlh_copy(bufs[0], bufs[1], n, stream), "copy")
+        check(hip.tlh_stream_synchronize(stream), "sync")
+    finally:
+        for b in bufs:
+            hip.tlh_free(b)
+    log(f"[bench] calibration copy of {mib} MiB done")
+
+
 def cpu_baseline(sample_batch: int, steps: int) -> dict:
     """The CPU oracle (single-threaded C++ restatement of the reference
     algorithms) running the same training step at a smaller batch."""
@@ -112,8 +154,13 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=2)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-sample-batch", type=int, default=4)
+    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager steps instead of hipGraph replays (for counter runs)")
+    ap.add_argument("--skip-d1024", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -134,15 +181,19 @@ def main() -> int:
     prog.synchronize()
     log(f"[bench] program ready: {prog.total} parameters, {tokens} tokens/step")
 
-    prog.capture(root, MAX_NORM)
+    if args.copy_calibration:
+        copy_calibration(hip, prog.stream, args.copy_calibration)
+    step = (lambda: prog.train_step(root, MAX_NORM)) if args.eager else prog.replay
+    if not args.eager:
+        prog.capture(root, MAX_NORM)
     for _ in range(args.warmup):
-        prog.replay()
+        step()
     prog.synchronize()
     log(f"[bench] {args.warmup} warmup steps done")
 
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        prog.replay()
+        step()
     prog.synchronize()
     dt = time.perf_counter() - t0
     ms_per_step = dt * 1e3 / args.steps
@@ -154,7 +205,7 @@ def main() -> int:
     prof = prog.profile_step(root, MAX_NORM)
     gemm_tflops = prof["gemm_flops"] / (prof["gemm_ms"] * 1e-3) / 1e12
     log(f"[bench] profiled step: {prof}")
-    d1024 = gemm_d1024(hip, prog.stream)
+    d1024 = None if args.skip_d1024 else gemm_d1024(hip, prog.stream)
     log(f"[bench] d=1024 GEMM: {d1024}")
     prog.close()
 
@@ -175,7 +226,8 @@ def main() -> int:
             "workload": "GPT training step (fwd + CE + bwd + clip 1.0 + AdamW), "
                         "vocab 2048, T 192, d 384, 4 blocks, 6 heads, FFN 1536, batch 32",
             "global_batch": CFG["batch"], "seq_len": CFG["seq"], "tokens_per_step": tokens,
-            "parallelism": "single GPU", "execution": "one hipGraph replay per step",
+            "parallelism": "single GPU",
+            "execution": "eager launches" if args.eager else "one hipGraph replay per step",
         },
         "roofline": {
             "bound": "mfma",
@@ -184,7 +236,10 @@ def main() -> int:
             "peak": FP32_MFMA_PEAK,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP32_MFMA_PEAK, 4),
-            "traffic": None,
+            "traffic": gemm_traffic(),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, "
+                            "profiles/gpt_step_b32_t192_d384_gemm_hbm_traffic.md)",
+            "algorithmic_bytes_per_launch": 36869625,
             "flops_per_step": prof["gemm_flops"],
             "launches_per_step": prof["gemm_launches"],
             "avg_launch_us": round(prof["gemm_ms"] * 1e3 / max(1, prof["gemm_launches"]), 2),

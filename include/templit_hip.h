@@ -226,7 +226,9 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * bm x bn tile (64 or 128 each), a K tile of bk (16 or 32) and, where a
  * workspace allows it, `splits` K splits; bm = bn = 0 restores the
  * automatic plan. Process-wide, for measurement sweeps. A forced split
- * count needs a workspace sized for it (tlh_gemm_workspace_size). */
+ * count needs a workspace sized for it (tlh_gemm_workspace_size).
+ * bk = -1 / -2 instead switches the XCD-aware block order off / on
+ * (default on) and leaves the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

@@ -46,6 +46,7 @@ struct GemmParams {
   int splits;
   int k_chunk;
   int tiles_n;
+  int xcd_remap;
 };
 
 __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
@@ -103,7 +104,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int r = lane & 31;
   const int hk = lane >> 5;
 
-  const int tile = blockIdx.x;
+  // Blocks are dispatched round-robin over the 8 XCDs (block x runs on XCD
+  // x % 8), each with its own L2. Give XCD j the contiguous tile range
+  // [j*G/8, (j+1)*G/8): tiles of the same tile row then share their A rows
+  // (and neighbouring rows their B columns) in one L2.
+  const int nblk = int(gridDim.x);
+  const int tile = (p.xcd_remap && (nblk & 7) == 0)
+                       ? int(blockIdx.x & 7) * (nblk >> 3) + int(blockIdx.x >> 3)
+                       : int(blockIdx.x);
   const int tm = tile / p.tiles_n;
   const int tn = tile - tm * p.tiles_n;
   const int m0 = tm * BM;
@@ -387,6 +395,7 @@ constexpr int kTargetBlocks = 256; // one block per CU at least
 // Process-wide plan override for tuning sweeps (tlh_gemm_set_plan); 0 = the
 // planner decides.
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
+int g_xcd_remap = 1;
 constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 
 // Tile plan, from measurements on MI355X of the GPT step's shapes
@@ -463,6 +472,7 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   }
   const Plan plan = make_plan(d, d.workspace != nullptr);
   p.tiles_n = (d.N + plan.bn - 1) / plan.bn;
+  p.xcd_remap = g_xcd_remap;
   const int tiles_m = (d.M + plan.bm - 1) / plan.bm;
   p.splits = plan.splits;
   p.k_chunk = p.splits > 1 ? ((d.K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : d.K;
@@ -525,6 +535,11 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
 } // namespace
 
 TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
+  // bk < 0 toggles the XCD-aware block order off (-1) or on (-2) instead.
+  if (bk == -1 || bk == -2) {
+    tlh::g_xcd_remap = bk == -2;
+    return 0;
+  }
   const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
   if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32)) return int(hipErrorInvalidValue);
   tlh::g_force_bm = bm;
