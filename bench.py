@@ -82,6 +82,61 @@ def gemm_d1024(hip, stream) -> dict:
             hip.tlh_free(b)
 
 
+SCALED = dict(vocab=2048, seq=1024, dim=1024, heads=16, layers=12, batch=8)
+EOS = 256  # the BPE tokeniser's end-of-sequence id (dataset/ tokens split on it)
+
+
+def scaled_gpt(steps: int, gen_tokens: int) -> dict:
+    """The scaled configuration: d 1024, 16 heads, 12 blocks, T 1024, V 2048,
+    batch 8 -- a training step (hipGraph replay) and greedy generation of
+    `gen_tokens` tokens from a 32-token random prompt (batch 1, the reference's
+    full-window recompute, and the equivalent valid-prefix recompute)."""
+    import numpy as np
+
+    from templit_amd.native import GptProgram
+
+    out: dict = {"config": dict(SCALED), "data": "synthetic: random tokens, N(0,0.02) weights"}
+    prog = GptProgram(**SCALED)
+    try:
+        tokens = SCALED["batch"] * SCALED["seq"]
+        prog.init_params(seed=21, std=0.02)
+        prog.set_optimizer(**HP)
+        prog.random_batch(seed=22)
+        prog.capture(1.0 / tokens, MAX_NORM)
+        for _ in range(2):
+            prog.replay()
+        prog.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            prog.replay()
+        prog.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        model_flops = 6.0 * prog.total * tokens  # excludes attention's T^2 term
+        out["train"] = {"tokens_per_step": tokens, "ms_per_step": round(dt * 1e3, 3),
+                        "tokens_per_s": round(tokens / dt, 1), "steps": steps,
+                        "loss": round(float(prog.losses().mean()), 4),
+                        "param_flops_tflops": round(model_flops / dt / 1e12, 2)}
+    finally:
+        prog.close()
+    log(f"[bench] scaled train: {out['train']}")
+    gen = GptProgram(**dict(SCALED, batch=1))
+    try:
+        gen.init_params(seed=21, std=0.02)
+        prompt = np.random.default_rng(23).integers(0, SCALED["vocab"], 32, dtype=np.uint32)
+        gen.generate_greedy(prompt, 2, EOS)  # warm-up
+        for mode, prefix in (("full_window", False), ("valid_prefix", True)):
+            t0 = time.perf_counter()
+            toks = gen.generate_greedy(prompt, gen_tokens, EOS, prefix_only=prefix)
+            dt = time.perf_counter() - t0
+            out[f"generate_{mode}"] = {"tokens": gen_tokens, "s": round(dt, 3),
+                                       "tokens_per_s": round(gen_tokens / dt, 2),
+                                       "first_tokens": [int(t) for t in toks[:8]]}
+    finally:
+        gen.close()
+    log(f"[bench] scaled generation: {out['generate_full_window']}, {out['generate_valid_prefix']}")
+    return out
+
+
 def gemm_traffic() -> float | None:
     """HBM bytes per GEMM launch from the committed counter profile (two
     rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, scaled by a copy of
@@ -159,6 +214,8 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="time eager steps instead of hipGraph replays (for counter runs)")
     ap.add_argument("--skip-d1024", action="store_true")
+    ap.add_argument("--skip-scaled", action="store_true",
+                    help="skip the d=1024 / 12-block / T=1024 configuration")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -248,6 +305,7 @@ def main() -> int:
             "eager_step_ms": round(prof["step_ms"], 4),
         },
         "gemm_d1024": d1024,
+        "scaled_gpt": None if args.skip_scaled else scaled_gpt(5, 256),
         "loss": round(loss, 4),
     }
     if not args.no_cpu_baseline:

@@ -82,6 +82,19 @@ int tlg_io(void *program, uint32_t **tokens, uint32_t **targets, float **losses,
 int tlg_train_step(void *program, float root_grad, float max_norm, int update);
 /* Forward only: logits [B*T, V] into the io logits buffer. */
 int tlg_forward(void *program);
+/* Greedy autoregressive generation (inference::autoregression,
+ * include/inference.h:45-99, with top_k = 1): the program must have
+ * batch 1; its window of `seq` tokens starts as the prompt followed by
+ * eos_token padding. Each of n_new steps runs the forward, takes the
+ * lowest-index argmax of the logits at the last valid position, appends it
+ * (sliding the window once full) and stores it in host_out[step]; EOS does
+ * not end generation. prefix_only = 0 recomputes the whole padded window
+ * as the reference does; 1 computes only the valid prefix, which gives the
+ * same logits because attention is causal. Synchronous. */
+int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
+                        uint32_t n_new, uint32_t eos_token, int prefix_only,
+                        uint32_t *host_out);
+
 /* Squared gradient norm of the last step (host read, synchronous). */
 int tlg_last_squared_norm(void *program, float *host_value);
 

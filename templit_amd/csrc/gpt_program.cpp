@@ -21,6 +21,7 @@
 #include "templit_gpt.h"
 #include "templit_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -36,6 +37,7 @@ struct Tensor {
 constexpr uint32_t kHeadDim = 64;
 constexpr float kRmsEps = 1e-6f; // src/my_metal/runtime.cpp:1044
 constexpr size_t kAlign = 64;    // floats: every tensor starts 256-byte aligned
+constexpr int kInvalidValue = 1; // hipErrorInvalidValue
 
 struct Program {
   tlg_config cfg{};
@@ -58,6 +60,7 @@ struct Program {
   // io
   uint32_t *tokens = nullptr, *targets = nullptr;
   float *losses = nullptr, *logits = nullptr, *dlogits = nullptr;
+  uint32_t *argmax_out = nullptr;
 
   // activations (per layer) and scratch
   std::vector<float *> x;        // L+1 residual-stream inputs [R,D]
@@ -173,26 +176,30 @@ int gemm(Program &p, tlh_gemm_desc d) {
   return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, p.stream); });
 }
 
-int forward(Program &p) {
+// Forward over the first `seq` <= cfg.seq positions of every sequence (the
+// whole window in training; a shorter prefix is exact for causal decoding,
+// where position t only sees positions <= t).
+int forward(Program &p, uint32_t seq) {
   const tlg_config &c = p.cfg;
-  const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
-  TRY(tlh_embedding_add_positions(p.P(0), c.vocab, p.P(1), p.tokens, c.batch, c.seq, c.dim,
+  const size_t rows = size_t(c.batch) * seq;
+  const int R = int(rows), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
+  TRY(tlh_embedding_add_positions(p.P(0), c.vocab, p.P(1), p.tokens, c.batch, seq, c.dim,
                                   p.x[0], p.stream));
   for (uint32_t l = 0; l < c.layers; ++l) {
     const uint32_t w = 2 + 12 * l;
-    TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, p.R, c.dim, kRmsEps, p.stream));
+    TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, rows, c.dim, kRmsEps, p.stream));
     float *qkv[3] = {p.q[l], p.k[l], p.v[l]};
     for (int j = 0; j < 3; ++j) {
       tlh_gemm_desc d = desc(p.n1[l], p.P(w + 2 * j), qkv[j], R, D, D, false, false);
       d.bias = p.P(w + 2 * j + 1);
-      d.remap_t = int(c.seq);
+      d.remap_t = int(seq);
       d.remap_h = int(c.heads);
       d.remap_d = int(kHeadDim);
       TRY(gemm(p, d));
     }
     TRY(timed(p, p.attn_spans, [&] {
       return tlh_attention_forward(p.q[l], p.k[l], p.v[l], p.o[l], p.lse[l], c.batch, c.heads,
-                                   c.seq, kHeadDim, 1.0f / std::sqrt(float(kHeadDim)), 1, 1,
+                                   seq, kHeadDim, 1.0f / std::sqrt(float(kHeadDim)), 1, 1,
                                    p.stream);
     }));
     {
@@ -201,7 +208,7 @@ int forward(Program &p) {
       d.residual = p.x[l];
       TRY(gemm(p, d));
     }
-    TRY(tlh_rms_norm(p.x_mid[l], nullptr, p.n2[l], nullptr, p.R, c.dim, kRmsEps, p.stream));
+    TRY(tlh_rms_norm(p.x_mid[l], nullptr, p.n2[l], nullptr, rows, c.dim, kRmsEps, p.stream));
     {
       tlh_gemm_desc d = desc(p.n2[l], p.P(w + 8), p.g[l], R, F, D, false, false);
       d.bias = p.P(w + 9);
@@ -216,7 +223,7 @@ int forward(Program &p) {
       TRY(gemm(p, d));
     }
   }
-  TRY(tlh_rms_norm(p.x[c.layers], nullptr, p.nf, nullptr, p.R, c.dim, kRmsEps, p.stream));
+  TRY(tlh_rms_norm(p.x[c.layers], nullptr, p.nf, nullptr, rows, c.dim, kRmsEps, p.stream));
   const uint32_t last = 2 + 12 * c.layers;
   tlh_gemm_desc d = desc(p.nf, p.P(last), p.logits, R, V, D, false, false);
   d.bias = p.P(last + 1);
@@ -286,7 +293,7 @@ int optimizer_step(Program &p, float max_norm) {
 }
 
 int train_step(Program &p, float root_grad, float max_norm, int update) {
-  TRY(forward(p));
+  TRY(forward(p, p.cfg.seq));
   TRY(tlh_cross_entropy_rows_fused(p.logits, p.targets, p.losses, p.dlogits, p.R, p.cfg.vocab,
                                    root_grad, p.stream));
   TRY(backward(p));
@@ -353,6 +360,7 @@ int create(Program &p) {
   TRY(tlh_fill_u32(p.tokens, 0, R, p.stream));
   TRY(tlh_fill_u32(p.targets, 0, R, p.stream));
   TRY(allocf(p, &p.losses, R));
+  TRY(alloc(p, reinterpret_cast<void **>(&p.argmax_out), sizeof(uint32_t)));
   TRY(allocf(p, &p.logits, R * V));
   TRY(allocf(p, &p.dlogits, R * V));
   p.x.resize(L + 1);
@@ -561,7 +569,44 @@ int tlg_train_step(void *program, float root_grad, float max_norm, int update) {
   return train_step(*static_cast<Program *>(program), root_grad, max_norm, update);
 }
 
-int tlg_forward(void *program) { return forward(*static_cast<Program *>(program)); }
+int tlg_forward(void *program) {
+  Program &p = *static_cast<Program *>(program);
+  return forward(p, p.cfg.seq);
+}
+
+int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
+                        uint32_t n_new, uint32_t eos_token, int prefix_only,
+                        uint32_t *host_out) {
+  Program &p = *static_cast<Program *>(program);
+  const tlg_config &c = p.cfg;
+  if (c.batch != 1 || prompt_len == 0 || prompt_len > c.seq) return kInvalidValue;
+  for (uint32_t i = 0; i < prompt_len; ++i)
+    if (host_prompt[i] >= c.vocab) return kInvalidValue;
+  // inference::autoregression (include/inference.h:45-99): the window holds
+  // the prompt, EOS-padded; each step recomputes the forward, predicts at
+  // the last valid position and appends (sliding once the window is full).
+  // Greedy = the lowest-index maximum of the logits; EOS does not stop it.
+  std::vector<uint32_t> context(c.seq, eos_token);
+  std::copy(host_prompt, host_prompt + prompt_len, context.begin());
+  uint32_t valid = prompt_len;
+  for (uint32_t g = 0; g < n_new; ++g) {
+    const uint32_t seq = prefix_only ? valid : c.seq;
+    TRY(tlh_memcpy_h2d(p.tokens, context.data(), size_t(seq) * sizeof(uint32_t), p.stream));
+    TRY(forward(p, seq));
+    TRY(tlh_argmax(p.logits + size_t(valid - 1) * c.vocab, c.vocab, p.argmax_out, p.stream));
+    uint32_t token = 0;
+    TRY(tlh_memcpy_d2h(&token, p.argmax_out, sizeof(token), p.stream));
+    TRY(tlh_stream_synchronize(p.stream));
+    host_out[g] = token;
+    if (valid < c.seq) {
+      context[valid++] = token;
+    } else {
+      std::move(context.begin() + 1, context.end(), context.begin());
+      context.back() = token;
+    }
+  }
+  return 0;
+}
 
 int tlg_last_squared_norm(void *program, float *host_value) {
   Program *p = static_cast<Program *>(program);

@@ -209,6 +209,7 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_io": [P, FP, FP, FP, FP],
     "tlg_train_step": [P, c_float, c_float, c_int],
     "tlg_forward": [P],
+    "tlg_generate_greedy": [P, P, c_uint32, c_uint32, c_uint32, c_int, P],
     "tlg_last_squared_norm": [P, POINTER(c_float)],
     "tlg_profile_step": [P, c_float, c_float, POINTER(c_float), POINTER(ctypes.c_double),
                          POINTER(c_uint32), POINTER(c_float), POINTER(c_float)],
@@ -362,6 +363,14 @@ class GptProgram:
 
     def forward(self):
         check(self.lib.tlg_forward(self.handle), "forward")
+
+    def generate_greedy(self, prompt, n_new, eos_token, prefix_only=False):
+        """Greedy tokens after `prompt` (inference::autoregression, top_k 1)."""
+        pr = self._np.ascontiguousarray(prompt, dtype=self._np.uint32)
+        out = self._np.empty(n_new, self._np.uint32)
+        check(self.lib.tlg_generate_greedy(self.handle, pr.ctypes.data, pr.size, n_new, eos_token,
+                                           int(prefix_only), out.ctypes.data), "generate")
+        return out
 
     def capture(self, root_grad, max_norm):
         check(self.lib.tlg_capture_train_step(self.handle, root_grad, max_norm), "capture")

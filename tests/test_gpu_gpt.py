@@ -188,3 +188,72 @@ def test_step_counters_start_at_zero_in_every_program():
             prog.synchronize()
         finally:
             prog.close()
+
+
+# ---------------------------------------------------------------------------
+# scaled architecture (d 1024, 16 heads of 64) and greedy generation
+# ---------------------------------------------------------------------------
+def test_scaled_width_step_matches_oracle():
+    # the d=1024 / 16-head block of the scaled config, 2 blocks, short window
+    cfg, params, tokens, targets = make_case(256, 128, 1024, 16, 2, 1, seed=500, std=0.02)
+    ref, got = run_both(cfg, params, tokens, targets, max_norm=1.0)
+    compare(cfg, ref, got)
+
+
+def _greedy_reference_check(cfg, params, prompt, generated, eos):
+    """Replays the generated tokens through the oracle's forward: every
+    token must be the lowest-index argmax of the oracle's logits at the last
+    valid position, up to ties within 1e-4 (the GPU's logits differ from
+    the oracle's by rounding only)."""
+    context = np.full(cfg.seq, eos, np.uint32)
+    context[:len(prompt)] = prompt
+    valid = len(prompt)
+    exact = 0
+    for tok in generated:
+        logits = O.gpt_forward(cfg, params, context)[valid - 1].astype(np.float64)
+        best = int(np.argmax(logits))
+        if tok == best:
+            exact += 1
+        else:
+            assert logits[best] - logits[tok] < 1e-4, (tok, best, logits[best] - logits[tok])
+        if valid < cfg.seq:
+            context[valid] = tok
+            valid += 1
+        else:
+            context = np.roll(context, -1)
+            context[-1] = tok
+    return exact
+
+
+@pytest.mark.parametrize("prefix_only", [False, True])
+def test_greedy_generation_matches_oracle(prefix_only):
+    V, T, D, H, L = 96, 32, 128, 2, 2
+    cfg = O.gpt_config(V, T, D, H, L, 1)
+    total = int(sum(O.gpt_param_sizes(cfg)))
+    params = O.normal((total,), 600, 0, 0.2)
+    prompt = O.uniform_u32((5,), 601, V)
+    eos = 7
+    prog = GptProgram(V, T, D, H, L, 1)
+    try:
+        prog.set_params(params)
+        out = prog.generate_greedy(prompt, 40, eos, prefix_only=prefix_only)  # slides past T
+    finally:
+        prog.close()
+    assert out.shape == (40,) and np.all(out < V)
+    assert _greedy_reference_check(cfg, params, prompt, out, eos) >= 38
+
+
+def test_greedy_prefix_equals_full_window():
+    V, T, D, H, L = 64, 48, 128, 2, 2
+    cfg = O.gpt_config(V, T, D, H, L, 1)
+    total = int(sum(O.gpt_param_sizes(cfg)))
+    params = O.normal((total,), 700, 0, 0.2)
+    prompt = O.uniform_u32((9,), 701, V)
+    prog = GptProgram(V, T, D, H, L, 1)
+    try:
+        prog.set_params(params)
+        full = prog.generate_greedy(prompt, 30, 0, prefix_only=False)
+        pref = prog.generate_greedy(prompt, 30, 0, prefix_only=True)
+    finally:
+        prog.close()
+    np.testing.assert_array_equal(full, pref)
