@@ -38,6 +38,8 @@ struct GemmDesc {
   uint32_t batch_stride_a[4] = {0, 0, 0, 0};
   uint32_t batch_stride_b[4] = {0, 0, 0, 0};
   uint32_t batch_stride_c[4] = {0, 0, 0, 0};
+  // Bias elements between consecutive batch entries (0: one shared bias).
+  uint32_t bias_batch_stride = 0;
   // Split-K (batch == 1 only, chosen by gemm_launch when a workspace is
   // given): partial products go to `workspace` ([splits, M, N] then
   // [splits, N] bias-gradient partials) and a reduction kernel applies the

@@ -47,6 +47,7 @@ struct GemmParams {
   int k_chunk;
   int tiles_n;
   int xcd_remap;
+  uint32_t bias_bstride; // bias elements between batch entries (batched launches)
 };
 
 __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
@@ -60,10 +61,10 @@ __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
 
 // Applies the epilogue to one output element. `C` already carries the batch
 // offset; bias/residual/aux are only used for batch == 1 (host-checked).
-__device__ inline void epilogue_store(const GemmParams &p, float *C, int m, int n,
-                                      float v) {
+__device__ inline void epilogue_store(const GemmParams &p, const float *bias, float *C, int m,
+                                      int n, float v) {
   const size_t idx = out_index(p, m, n);
-  if (p.bias) v += p.bias[n];
+  if (bias) v += bias[n];
   if (p.beta != 0.0f) v += p.beta * C[idx];
   if (p.residual) v += p.residual[idx];
   if (p.epilogue == kEpiGelu) {
@@ -117,9 +118,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
+  // (p stays unmodified: writing a kernel-argument struct that is also
+  // passed by reference moves it to scratch memory)
   const float *A = p.A;
   const float *B = p.B;
   float *C = p.C;
+  const float *bias = p.bias;
   int k_begin = 0, k_end = p.K;
   if (p.splits > 1) {
     k_begin = blockIdx.z * p.k_chunk;
@@ -138,6 +142,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     A += oa;
     B += ob;
     C += oc;
+    if (bias) bias += size_t(blockIdx.z) * p.bias_bstride;
   }
 
   // ---- global -> register prefetch ----------------------------------------
@@ -331,7 +336,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
         if (p.splits > 1) {
           C[size_t(m) * p.N + n] = acc[i][j][v];
         } else {
-          epilogue_store(p, C, m, n, acc[i][j][v]);
+          epilogue_store(p, bias, C, m, n, acc[i][j][v]);
         }
       }
     }
@@ -339,19 +344,42 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 }
 
 // Sums the split-K partials and applies the epilogue; deterministic order.
+// VEC4: the plane is read as float4 (N % 4 == 0, so the 4 elements of a
+// float4 share a row) with the split loop unrolled for loads in flight.
+template <bool VEC4>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
   const size_t plane = size_t(p.M) * p.N;
-  const size_t total = plane + (p.bias_grad ? size_t(p.N) : 0);
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += size_t(gridDim.x) * blockDim.x) {
-    if (i < plane) {
+  const size_t step = size_t(gridDim.x) * blockDim.x;
+  const size_t tid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if constexpr (VEC4) {
+    const f4 *w = reinterpret_cast<const f4 *>(p.workspace);
+    const size_t plane4 = plane / 4;
+    for (size_t i = tid; i < plane4; i += step) {
+      f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+      int z = 0;
+      for (; z + 1 < p.splits; z += 2) {
+        const f4 a = w[size_t(z) * plane4 + i], b = w[size_t(z + 1) * plane4 + i];
+        s0 += a;
+        s1 += b;
+      }
+      if (z < p.splits) s0 += w[size_t(z) * plane4 + i];
+      const f4 sum = s0 + s1;
+      const int m = int((i * 4) / p.N);
+      const int n = int(i * 4 - size_t(m) * p.N);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) epilogue_store(p, p.bias, p.C, m, n + e, sum[e]);
+    }
+  } else {
+    for (size_t i = tid; i < plane; i += step) {
       float s = 0.f;
       for (int z = 0; z < p.splits; ++z) s += p.workspace[z * plane + i];
       const int m = int(i / p.N);
       const int n = int(i - size_t(m) * p.N);
-      epilogue_store(p, p.C, m, n, s);
-    } else {
-      const size_t n = i - plane;
+      epilogue_store(p, p.bias, p.C, m, n, s);
+    }
+  }
+  if (p.bias_grad) {
+    for (size_t n = tid; n < size_t(p.N); n += step) {
       float s = 0.f;
       for (int z = 0; z < p.splits; ++z) s += p.workspace[size_t(p.splits) * plane + z * size_t(p.N) + n];
       p.bias_grad[n] = p.beta != 0.0f ? s + p.beta * p.bias_grad[n] : s;
@@ -464,6 +492,7 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.epilogue = d.epilogue;
   p.remap_t = d.remap_t; p.remap_h = d.remap_h; p.remap_d = d.remap_d;
   p.batch_ndim = d.batch_ndim;
+  p.bias_bstride = d.bias_batch_stride;
   for (int i = 0; i < 4; ++i) {
     p.batch_shape[i] = d.batch_shape[i];
     p.bsa[i] = d.batch_stride_a[i];
@@ -480,7 +509,7 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   const size_t reduce_elems = size_t(d.M) * d.N + (d.bias_grad ? d.N : 0);
   if (d.K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
-    gemm_splitk_reduce<<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
+    gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     return launch_status();
   }
   const int z = p.splits > 1 ? p.splits : std::max(1, d.batch);
@@ -504,7 +533,12 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   int st = launch_status();
   if (st) return st;
   if (p.splits > 1) {
-    gemm_splitk_reduce<<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
+    // The workspace planes start 16-byte aligned when M*N is a multiple of 4.
+    const bool v4 = d.N % 4 == 0 && (reinterpret_cast<uintptr_t>(d.workspace) & 15) == 0;
+    if (v4)
+      gemm_splitk_reduce<true><<<stride_grid(reduce_elems / 4 + 1, 256), 256, 0, s>>>(p);
+    else
+      gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     st = launch_status();
   }
   return st;
@@ -530,6 +564,15 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
   d.epilogue = c.epilogue;
   d.remap_t = c.remap_t; d.remap_h = c.remap_h; d.remap_d = c.remap_d;
   d.bias_grad = c.bias_grad;
+  if (c.batch > 1) {
+    d.batch = c.batch;
+    d.batch_ndim = 1;
+    d.batch_shape[0] = uint32_t(c.batch);
+    d.batch_stride_a[0] = c.batch_stride_a;
+    d.batch_stride_b[0] = c.batch_stride_b;
+    d.batch_stride_c[0] = c.batch_stride_c;
+    d.bias_batch_stride = c.bias_batch_stride;
+  }
   return d;
 }
 } // namespace
@@ -557,6 +600,8 @@ TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
     return int(hipErrorInvalidValue);
   if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 || d.M % d.remap_t ||
                         d.N != d.remap_h * d.remap_d))
+    return int(hipErrorInvalidValue);
+  if (desc->batch > 1 && (d.residual || d.aux || d.bias_grad || d.epilogue != tlh::kEpiStore))
     return int(hipErrorInvalidValue);
   return tlh::gemm_launch(d, stream);
 }

@@ -172,7 +172,7 @@ tlh_gemm_desc wgrad(const float *x, const float *dy, float *dw, float *db, int i
 
 int gemm(Program &p, tlh_gemm_desc d) {
   if (d.trans_a) d.workspace = p.workspace; // tall-K weight gradients may split K
-  if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k;
+  if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k * (d.batch > 1 ? d.batch : 1);
   return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, p.stream); });
 }
 
@@ -188,13 +188,20 @@ int forward(Program &p, uint32_t seq) {
   for (uint32_t l = 0; l < c.layers; ++l) {
     const uint32_t w = 2 + 12 * l;
     TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, rows, c.dim, kRmsEps, p.stream));
-    float *qkv[3] = {p.q[l], p.k[l], p.v[l]};
-    for (int j = 0; j < 3; ++j) {
-      tlh_gemm_desc d = desc(p.n1[l], p.P(w + 2 * j), qkv[j], R, D, D, false, false);
-      d.bias = p.P(w + 2 * j + 1);
+    {
+      // Q, K and V in one batched launch: the three weights (and biases)
+      // sit at a constant stride in the parameter buffer and q, k, v are
+      // consecutive planes of one allocation.
+      tlh_gemm_desc d = desc(p.n1[l], p.P(w), p.q[l], R, D, D, false, false);
+      d.bias = p.P(w + 1);
       d.remap_t = int(seq);
       d.remap_h = int(c.heads);
       d.remap_d = int(kHeadDim);
+      d.batch = 3;
+      d.batch_stride_a = 0;
+      d.batch_stride_b = uint32_t(p.P(w + 2) - p.P(w));
+      d.batch_stride_c = uint32_t(p.k[l] - p.q[l]);
+      d.bias_batch_stride = uint32_t(p.P(w + 3) - p.P(w + 1));
       TRY(gemm(p, d));
     }
     TRY(timed(p, p.attn_spans, [&] {
@@ -365,9 +372,18 @@ int create(Program &p) {
   TRY(allocf(p, &p.dlogits, R * V));
   p.x.resize(L + 1);
   for (auto &b : p.x) TRY(allocf(p, &b, R * D));
-  for (auto *vec : {&p.n1, &p.q, &p.k, &p.v, &p.o, &p.x_mid, &p.n2}) {
+  for (auto *vec : {&p.n1, &p.o, &p.x_mid, &p.n2}) {
     vec->resize(L);
     for (auto &b : *vec) TRY(allocf(p, &b, R * D));
+  }
+  // q, k, v of a layer: three consecutive [B,H,T,64] planes (one batched GEMM)
+  p.q.resize(L);
+  p.k.resize(L);
+  p.v.resize(L);
+  for (size_t l = 0; l < L; ++l) {
+    TRY(allocf(p, &p.q[l], 3 * R * D));
+    p.k[l] = p.q[l] + R * D;
+    p.v[l] = p.q[l] + 2 * R * D;
   }
   p.lse.resize(L);
   for (auto &b : p.lse) TRY(allocf(p, &b, B * H * T));
@@ -396,6 +412,14 @@ int create(Program &p) {
     if (e > ws) ws = e;
   }
   p.workspace_elems = ws;
+  // The batched Q/K/V GEMM needs wq->wk->wv (and bq->bk->bv) at one stride;
+  // every tensor is padded to kAlign floats and D is a multiple of 64.
+  for (size_t l = 0; l < L; ++l) {
+    const uint32_t w = 2 + 12 * uint32_t(l);
+    if (p.offset[w + 2] - p.offset[w] != p.offset[w + 4] - p.offset[w + 2] ||
+        p.offset[w + 3] - p.offset[w + 1] != p.offset[w + 5] - p.offset[w + 3])
+      return kInvalidValue;
+  }
   if (ws) TRY(allocf(p, &p.workspace, ws));
   p.lr = 1e-3f;
   TRY(write_scalars(p, 0.9f, 0.999f));

@@ -34,6 +34,9 @@ class GemmDesc(ctypes.Structure):
         ("epilogue", c_int32),
         ("remap_t", c_int32), ("remap_h", c_int32), ("remap_d", c_int32),
         ("bias_grad", c_void_p),
+        ("batch", c_int32),
+        ("batch_stride_a", c_uint32), ("batch_stride_b", c_uint32),
+        ("batch_stride_c", c_uint32), ("bias_batch_stride", c_uint32),
     ]
 
 
