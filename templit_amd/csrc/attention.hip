@@ -45,19 +45,32 @@ __device__ inline f16x mfma(float a, float b, const f16x &c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// Cooperative load of rows [r0, r0+64) of a [T, 64] head matrix into an LDS
-// tile with row stride LDP; rows >= T are zero.
-__device__ inline void load_tile(float *tile, const float *src_base, const Dims &d, uint32_t b,
-                                 uint32_t h, int r0, int merged) {
-  // 64 rows x 16 float4 = 1024 float4, 4 per thread.
+// Rows [r0, r0+64) of a [T, 64] head matrix held by the block's 256 threads
+// (4 float4 each; rows >= T are zero): fetched from global memory into
+// registers while the previous tile is being used, then put into LDS.
+struct TileRegs {
+  f4 v[4];
+};
+
+__device__ inline void fetch_tile(TileRegs &t, const float *src_base, const Dims &d, uint32_t b,
+                                  uint32_t h, int r0, int merged) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int idx = threadIdx.x + i * 256;
     const int row = idx >> 4, c4 = idx & 15;
-    const int t = r0 + row;
+    const int tt = r0 + row;
     f4 v = {0.f, 0.f, 0.f, 0.f};
-    if (t < int(d.T)) v = *reinterpret_cast<const f4 *>(src_base + row_off(d, b, h, t, merged) + c4 * 4);
-    *reinterpret_cast<f4 *>(tile + row * LDP + c4 * 4) = v;
+    if (tt < int(d.T)) v = *reinterpret_cast<const f4 *>(src_base + row_off(d, b, h, tt, merged) + c4 * 4);
+    t.v[i] = v;
+  }
+}
+
+__device__ inline void put_tile(float *tile, const TileRegs &t) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = threadIdx.x + i * 256;
+    const int row = idx >> 4, c4 = idx & 15;
+    *reinterpret_cast<f4 *>(tile + row * LDP + c4 * 4) = t.v[i];
   }
 }
 
@@ -132,12 +145,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
   const int q_end = min(int(d.T), q_block + BQ);
   const int k_end = causal ? q_end : int(d.T);
   const int nkb = (k_end + KB - 1) / KB;
+  // K/V tile kb+1 is fetched into registers while tile kb is in use.
+  TileRegs kpre, vpre;
+  fetch_tile(kpre, k, d, b, h, 0, 0);
+  fetch_tile(vpre, v, d, b, h, 0, 0);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * KB;
+    __syncthreads(); // every wave is done with the previous tile
+    put_tile(Ks, kpre);
+    put_tile(Vs, vpre);
     __syncthreads();
-    load_tile(Ks, k, d, b, h, k0, 0);
-    load_tile(Vs, v, d, b, h, k0, 0);
-    __syncthreads();
+    if (kb + 1 < nkb) {
+      fetch_tile(kpre, k, d, b, h, k0 + KB, 0);
+      fetch_tile(vpre, v, d, b, h, k0 + KB, 0);
+    }
     if (!active || (causal && k0 > q0 + WQ - 1)) continue;
     f16x st[2];
 #pragma unroll
@@ -264,16 +285,31 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_kernel(
 
   const size_t lse_base = (size_t(b) * d.H + h) * d.T;
   const int q_start = causal ? (k_block / KB) * KB : 0;
+  // Q/dO tile (and its lse, delta) qt0+KB is fetched while qt0 is in use.
+  TileRegs qpre, dopre;
+  float lse_pre = 0.f, delta_pre = 0.f;
+  auto fetch_q = [&](int qt0) {
+    fetch_tile(qpre, q, d, b, h, qt0, 0);
+    fetch_tile(dopre, dout, d, b, h, qt0, o_merged);
+    const int t = qt0 + int(threadIdx.x);
+    if (threadIdx.x < KB && t < int(d.T)) {
+      lse_pre = lse[lse_base + t];
+      delta_pre = delta[lse_base + t];
+    } else {
+      lse_pre = delta_pre = 0.f;
+    }
+  };
+  if (q_start < int(d.T)) fetch_q(q_start);
   for (int qt0 = q_start; qt0 < int(d.T); qt0 += KB) {
-    __syncthreads();
-    load_tile(Qs, q, d, b, h, qt0, 0);
-    load_tile(dOs, dout, d, b, h, qt0, o_merged);
+    __syncthreads(); // every wave is done with the previous tile
+    put_tile(Qs, qpre);
+    put_tile(dOs, dopre);
     if (threadIdx.x < KB) {
-      const int t = qt0 + threadIdx.x;
-      lse_s[threadIdx.x] = t < int(d.T) ? lse[lse_base + t] : 0.f;
-      delta_s[threadIdx.x] = t < int(d.T) ? delta[lse_base + t] : 0.f;
+      lse_s[threadIdx.x] = lse_pre;
+      delta_s[threadIdx.x] = delta_pre;
     }
     __syncthreads();
+    if (qt0 + KB < int(d.T)) fetch_q(qt0 + KB);
     if (!active || (causal && qt0 + KB - 1 < key0)) continue;
     // S[q][key] for 64 queries (mt) x 32 keys
     f16x sp[2], dp[2];
@@ -378,12 +414,19 @@ __global__ __launch_bounds__(256) void attn_bwd_q_kernel(
   const int q_end = min(int(d.T), q_block + BQ);
   const int k_end = causal ? q_end : int(d.T);
   const int nkb = (k_end + KB - 1) / KB;
+  TileRegs kpre, vpre;
+  fetch_tile(kpre, k, d, b, h, 0, 0);
+  fetch_tile(vpre, v, d, b, h, 0, 0);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * KB;
+    __syncthreads(); // every wave is done with the previous tile
+    put_tile(Ks, kpre);
+    put_tile(Vs, vpre);
     __syncthreads();
-    load_tile(Ks, k, d, b, h, k0, 0);
-    load_tile(Vs, v, d, b, h, k0, 0);
-    __syncthreads();
+    if (kb + 1 < nkb) {
+      fetch_tile(kpre, k, d, b, h, k0 + KB, 0);
+      fetch_tile(vpre, v, d, b, h, k0 + KB, 0);
+    }
     if (!active || (causal && k0 > q0 + WQ - 1)) continue;
     f16x st[2], dpt[2];
 #pragma unroll
