@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const float *__restrict
 // queries q(v,h) of key r: the A-operand layout of P^T / dS^T for
 // dV = P^T.dO and dK = dS^T.Q.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_bwd_kv_kernel(
+__global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv, Dims d,
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_kernel(
 // LDS (as in the forward). dQ^T = K^T.dS^T uses dS^T straight from the
 // S^T-layout registers as the B operand.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_bwd_q_kernel(
+__global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dq, Dims d, float scale, int causal,
