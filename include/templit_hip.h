@@ -217,12 +217,17 @@ typedef struct tlh_gemm_desc {
    * sum_to_shape of dY to [1,N], runtime.cpp:661-739), computed from the dY
    * tiles the GEMM already stages in LDS. Not with remap_* or batching. */
   float *bias_grad;
-  /* Batched form (batch > 1): gridDim.z = batch, and entry z reads
-   * a + z*batch_stride_a, b + z*batch_stride_b, bias + z*bias_batch_stride
-   * and writes c + z*batch_stride_c (element strides; 0 shares an operand).
-   * Not with bias_grad or split-K. batch <= 1 is the single product. */
+  /* Batched form (batch > 1): entry z reads a + z*batch_stride_a,
+   * b + z*batch_stride_b, bias + z*bias_batch_stride and writes
+   * c + z*batch_stride_c and bias_grad + z*bias_batch_stride (element
+   * strides; 0 shares an operand). No residual, aux or GELU epilogue.
+   * With sum_batches != 0 the entries are instead summed into one c:
+   * c = sum_z op(A_z).op(B_z) (+bias, +beta*c, +residual once), i.e. one
+   * product over K*batch whose K range z uses operands z (k must be a
+   * multiple of 32; no bias_grad). batch <= 1 is the single product. */
   int32_t batch;
   uint32_t batch_stride_a, batch_stride_b, batch_stride_c, bias_batch_stride;
+  int32_t sum_batches;
 } tlh_gemm_desc;
 
 int tlh_gemm(const tlh_gemm_desc *desc, void *stream);

@@ -38,8 +38,13 @@ struct GemmDesc {
   uint32_t batch_stride_a[4] = {0, 0, 0, 0};
   uint32_t batch_stride_b[4] = {0, 0, 0, 0};
   uint32_t batch_stride_c[4] = {0, 0, 0, 0};
-  // Bias elements between consecutive batch entries (0: one shared bias).
+  // Bias (and bias-gradient) elements between consecutive batch entries
+  // (0: one shared bias).
   uint32_t bias_batch_stride = 0;
+  // The batch entries (1-D batch) are K-partials of one product: each entry
+  // multiplies its own A and B and the results are summed into C (with the
+  // epilogue applied once). Needs a workspace; no bias gradient.
+  int sum_batches = 0;
   // Split-K (batch == 1 only, chosen by gemm_launch when a workspace is
   // given): partial products go to `workspace` ([splits, M, N] then
   // [splits, N] bias-gradient partials) and a reduction kernel applies the

@@ -47,7 +47,12 @@ struct GemmParams {
   int k_chunk;
   int tiles_n;
   int xcd_remap;
-  uint32_t bias_bstride; // bias elements between batch entries (batched launches)
+  uint32_t bias_bstride; // bias (and bias-gradient) elements between batch entries
+  int batch;             // output entries (blockIdx.z = entry * splits + split)
+  // K-segmented operands (summed batch entries): K index k lies in segment
+  // k / seg_k, whose A and B start seg_a / seg_b elements further on.
+  int seg_k;
+  uint32_t seg_a, seg_b;
 };
 
 __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
@@ -124,13 +129,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const float *B = p.B;
   float *C = p.C;
   const float *bias = p.bias;
+  // blockIdx.z = output entry * splits + split (a split is a K range).
+  const int zs = p.splits > 1 ? int(blockIdx.z) % p.splits : 0;
+  const int zb = p.splits > 1 ? int(blockIdx.z) / p.splits : int(blockIdx.z);
+  float *bias_grad = p.bias_grad;
   int k_begin = 0, k_end = p.K;
-  if (p.splits > 1) {
-    k_begin = blockIdx.z * p.k_chunk;
-    k_end = min(p.K, k_begin + p.k_chunk);
-    C = p.workspace + size_t(blockIdx.z) * p.M * p.N;
-  } else if (p.batch_ndim > 0) {
-    uint32_t rem = blockIdx.z;
+  if (p.batch_ndim > 0) {
+    uint32_t rem = uint32_t(zb);
     size_t oa = 0, ob = 0, oc = 0;
     for (int d = p.batch_ndim - 1; d >= 0; --d) {
       const uint32_t c = rem % p.batch_shape[d];
@@ -142,13 +147,28 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     A += oa;
     B += ob;
     C += oc;
-    if (bias) bias += size_t(blockIdx.z) * p.bias_bstride;
+    if (bias) bias += size_t(zb) * p.bias_bstride;
+    if (bias_grad) bias_grad += size_t(zb) * p.bias_bstride;
+  }
+  if (p.splits > 1) {
+    k_begin = zs * p.k_chunk;
+    k_end = min(p.K, k_begin + p.k_chunk);
+    C = p.workspace + (size_t(zb) * p.splits + zs) * p.M * p.N;
   }
 
   // ---- global -> register prefetch ----------------------------------------
   f4 ra[A_CHUNKS], rb[B_CHUNKS];
 
   auto load_tile = [&](int k0) {
+    // K tiles never straddle a segment (seg_k is a multiple of the K tile)
+    const float *As = A, *Bs = B;
+    int kofs = 0; // global k minus the segment-local k
+    if (p.seg_k > 0) {
+      const int sg = k0 / p.seg_k;
+      kofs = sg * p.seg_k;
+      As += size_t(sg) * p.seg_a;
+      Bs += size_t(sg) * p.seg_b;
+    }
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
       const int c = tid + i * 256;
@@ -159,7 +179,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int gcol = TA ? (m0 + col) : (k0 + col);
       const int row_lim = TA ? k_end : p.M;
       const int col_lim = TA ? p.M : k_end;
-      const float *src = A + size_t(grow) * p.lda + gcol;
+      const float *src = As + size_t(TA ? grow - kofs : grow) * p.lda + (TA ? gcol : gcol - kofs);
       if constexpr (FULL) {
         ra[i] = *reinterpret_cast<const f4 *>(src);
       } else {
@@ -186,7 +206,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int gcol = TB ? (k0 + col) : (n0 + col);
       const int row_lim = TB ? p.N : k_end;
       const int col_lim = TB ? k_end : p.N;
-      const float *src = B + size_t(grow) * p.ldb + gcol;
+      const float *src = Bs + size_t(TB ? grow : grow - kofs) * p.ldb + (TB ? gcol - kofs : gcol);
       if constexpr (FULL) {
         rb[i] = *reinterpret_cast<const f4 *>(src);
       } else {
@@ -315,9 +335,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
       for (int g = 0; g < BGROUPS; ++g) t += smem[g * BN + tid];
       if (p.splits > 1) {
-        p.workspace[size_t(p.splits) * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
+        p.workspace[size_t(p.batch) * p.splits * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
       } else {
-        p.bias_grad[n] = p.beta != 0.0f ? t + p.beta * p.bias_grad[n] : t;
+        bias_grad[n] = p.beta != 0.0f ? t + p.beta * bias_grad[n] : t;
       }
     }
   }
@@ -343,7 +363,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   }
 }
 
-// Sums the split-K partials and applies the epilogue; deterministic order.
+// Sums the split-K partials of every output entry in split order --
+// deterministic -- and applies the epilogue.
 // VEC4: the plane is read as float4 (N % 4 == 0, so the 4 elements of a
 // float4 share a row) with the split loop unrolled for loads in flight.
 template <bool VEC4>
@@ -351,38 +372,50 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
   const size_t plane = size_t(p.M) * p.N;
   const size_t step = size_t(gridDim.x) * blockDim.x;
   const size_t tid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if constexpr (VEC4) {
-    const f4 *w = reinterpret_cast<const f4 *>(p.workspace);
-    const size_t plane4 = plane / 4;
-    for (size_t i = tid; i < plane4; i += step) {
-      f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-      int z = 0;
-      for (; z + 1 < p.splits; z += 2) {
-        const f4 a = w[size_t(z) * plane4 + i], b = w[size_t(z + 1) * plane4 + i];
-        s0 += a;
-        s1 += b;
-      }
-      if (z < p.splits) s0 += w[size_t(z) * plane4 + i];
-      const f4 sum = s0 + s1;
-      const int m = int((i * 4) / p.N);
-      const int n = int(i * 4 - size_t(m) * p.N);
+  const int entries = p.batch;
+  for (int b = 0; b < entries; ++b) {
+    float *C = p.C;
+    const float *bias = p.bias;
+    if (p.batch_ndim > 0) {
+      C += size_t(b) * p.bsc[0];
+      if (bias) bias += size_t(b) * p.bias_bstride;
+    }
+    const float *ws = p.workspace + size_t(b) * p.splits * plane;
+    if constexpr (VEC4) {
+      const f4 *w = reinterpret_cast<const f4 *>(ws);
+      const size_t plane4 = plane / 4;
+      for (size_t i = tid; i < plane4; i += step) {
+        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+        int z = 0;
+        for (; z + 1 < p.splits; z += 2) {
+          const f4 a = w[size_t(z) * plane4 + i], c = w[size_t(z + 1) * plane4 + i];
+          s0 += a;
+          s1 += c;
+        }
+        if (z < p.splits) s0 += w[size_t(z) * plane4 + i];
+        const f4 sum = s0 + s1;
+        const int m = int((i * 4) / p.N);
+        const int n = int(i * 4 - size_t(m) * p.N);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) epilogue_store(p, p.bias, p.C, m, n + e, sum[e]);
+        for (int e = 0; e < 4; ++e) epilogue_store(p, bias, C, m, n + e, sum[e]);
+      }
+    } else {
+      for (size_t i = tid; i < plane; i += step) {
+        float s = 0.f;
+        for (int z = 0; z < p.splits; ++z) s += ws[z * plane + i];
+        const int m = int(i / p.N);
+        const int n = int(i - size_t(m) * p.N);
+        epilogue_store(p, bias, C, m, n, s);
+      }
     }
-  } else {
-    for (size_t i = tid; i < plane; i += step) {
-      float s = 0.f;
-      for (int z = 0; z < p.splits; ++z) s += p.workspace[z * plane + i];
-      const int m = int(i / p.N);
-      const int n = int(i - size_t(m) * p.N);
-      epilogue_store(p, p.bias, p.C, m, n, s);
-    }
-  }
-  if (p.bias_grad) {
-    for (size_t n = tid; n < size_t(p.N); n += step) {
-      float s = 0.f;
-      for (int z = 0; z < p.splits; ++z) s += p.workspace[size_t(p.splits) * plane + z * size_t(p.N) + n];
-      p.bias_grad[n] = p.beta != 0.0f ? s + p.beta * p.bias_grad[n] : s;
+    if (p.bias_grad) {
+      float *bg = p.bias_grad + (p.batch_ndim > 0 ? size_t(b) * p.bias_bstride : 0);
+      const float *wb = p.workspace + size_t(entries) * p.splits * plane + size_t(b) * p.splits * p.N;
+      for (size_t n = tid; n < size_t(p.N); n += step) {
+        float s = 0.f;
+        for (int z = 0; z < p.splits; ++z) s += wb[z * size_t(p.N) + n];
+        bg[n] = p.beta != 0.0f ? s + p.beta * bg[n] : s;
+      }
     }
   }
 }
@@ -435,18 +468,20 @@ constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 //  - tall-K products (weight gradients, K = B*T) with too few output tiles
 //    split K so that about 1024 blocks run, each with K chunks of >= 256.
 Plan make_plan(const GemmDesc &d, bool allow_split) {
+  // Summed batch entries are one product over the folded K (see gemm_launch).
+  const size_t outputs = d.sum_batches ? 1 : size_t(std::max(1, d.batch));
+  const int K = d.sum_batches ? d.K * d.batch : d.K;
+  const bool one_dim = d.sum_batches || d.batch_ndim <= 1;
   if (g_force_bm > 0) {
-    const bool can_split = allow_split && d.batch <= 1 && d.batch_ndim == 0;
+    const bool can_split = allow_split && one_dim;
     return {g_force_bm, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, g_force_bk};
   }
-  const size_t batch = size_t(std::max(1, d.batch));
-  if (tiles_for(d, 128, 128) * batch >= 3 * size_t(kTargetBlocks)) return {128, 128, 1, 16};
-  const size_t tiles = tiles_for(d, 64, 64);
-  if (allow_split && batch == 1 && d.batch_ndim == 0 && tiles * 4 < 4 * size_t(kTargetBlocks) &&
-      d.K >= 2 * kMinSplitK) {
+  if (tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks)) return {128, 128, 1, 16};
+  const size_t tiles = tiles_for(d, 64, 64) * outputs;
+  if (allow_split && one_dim && tiles < size_t(kTargetBlocks) && K >= 2 * kMinSplitK) {
     int splits = 1;
     while (splits < 16 && tiles * size_t(splits) < 4 * size_t(kTargetBlocks) &&
-           d.K / (splits * 2) >= kMinSplitK)
+           K / (splits * 2) >= kMinSplitK)
       splits *= 2;
     if (splits >= 2) return {64, 64, splits, 32};
   }
@@ -472,13 +507,19 @@ int gemm_choose_splits(const GemmDesc &d) { return make_plan(d, true).splits; }
 
 size_t gemm_workspace_elems(const GemmDesc &d) {
   const int s = gemm_choose_splits(d);
-  // C partials [s, M, N] followed by bias-gradient partials [s, N]
-  return s > 1 ? size_t(s) * (size_t(d.M) * d.N + d.N) : 0;
+  const size_t outputs = d.sum_batches ? 1 : size_t(std::max(1, d.batch));
+  // C partials [outputs, s, M, N] followed by bias-gradient partials
+  // [outputs, s, N]
+  return s > 1 ? outputs * size_t(s) * (size_t(d.M) * d.N + d.N) : 0;
 }
 
 int gemm_launch(const GemmDesc &d, void *stream) {
   if (d.M <= 0 || d.N <= 0) return 0;
-  if (d.bias_grad && (d.batch > 1 || d.batch_ndim > 0 || d.remap_h > 0))
+  if (d.bias_grad && (d.batch_ndim > 1 || d.remap_h > 0 || d.sum_batches))
+    return int(hipErrorInvalidValue);
+  // Summed batch entries: K segments of kBK-multiple length (a K tile never
+  // straddles two entries' operands).
+  if (d.sum_batches && (d.batch < 2 || d.batch_ndim != 1 || d.K % kBK))
     return int(hipErrorInvalidValue);
   hipStream_t s = as_stream(stream);
   GemmParams p{};
@@ -493,6 +534,17 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.remap_t = d.remap_t; p.remap_h = d.remap_h; p.remap_d = d.remap_d;
   p.batch_ndim = d.batch_ndim;
   p.bias_bstride = d.bias_batch_stride;
+  p.batch = std::max(1, d.batch);
+  int K = d.K;
+  if (d.sum_batches) { // fold the batch into K: one product over batch*K
+    K = d.K * d.batch;
+    p.K = K;
+    p.seg_k = d.K;
+    p.seg_a = d.batch_stride_a[0];
+    p.seg_b = d.batch_stride_b[0];
+    p.batch = 1;
+    p.batch_ndim = 0;
+  }
   for (int i = 0; i < 4; ++i) {
     p.batch_shape[i] = d.batch_shape[i];
     p.bsa[i] = d.batch_stride_a[i];
@@ -504,20 +556,20 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.xcd_remap = g_xcd_remap;
   const int tiles_m = (d.M + plan.bm - 1) / plan.bm;
   p.splits = plan.splits;
-  p.k_chunk = p.splits > 1 ? ((d.K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : d.K;
-  if (p.splits > 1) p.splits = (d.K + p.k_chunk - 1) / p.k_chunk; // <= plan.splits
-  const size_t reduce_elems = size_t(d.M) * d.N + (d.bias_grad ? d.N : 0);
-  if (d.K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
+  p.k_chunk = p.splits > 1 ? ((K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : K;
+  if (p.splits > 1) p.splits = (K + p.k_chunk - 1) / p.k_chunk; // <= plan.splits
+  const size_t reduce_elems = size_t(d.M) * d.N;
+  if (K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
     gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     return launch_status();
   }
-  const int z = p.splits > 1 ? p.splits : std::max(1, d.batch);
+  const int z = p.splits > 1 ? p.batch * p.splits : p.batch;
   dim3 grid(unsigned(tiles_m * p.tiles_n), 1, unsigned(z));
   const bool ta = d.trans_a != 0, tb = d.trans_b != 0, vec = vec_ok(d);
   // Every block's K range is a multiple of the K tile when K is and the
   // split chunk (a multiple of kBK) is.
-  const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && d.K % plan.bk == 0 &&
+  const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && K % plan.bk == 0 &&
                     (p.splits <= 1 || p.k_chunk % plan.bk == 0);
   if (plan.bk == 32) {
     if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64, 32>(p, ta, tb, vec, full, grid, s);
@@ -572,6 +624,7 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
     d.batch_stride_b[0] = c.batch_stride_b;
     d.batch_stride_c[0] = c.batch_stride_c;
     d.bias_batch_stride = c.bias_batch_stride;
+    d.sum_batches = c.sum_batches != 0;
   }
   return d;
 }
@@ -601,7 +654,8 @@ TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
   if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 || d.M % d.remap_t ||
                         d.N != d.remap_h * d.remap_d))
     return int(hipErrorInvalidValue);
-  if (desc->batch > 1 && (d.residual || d.aux || d.bias_grad || d.epilogue != tlh::kEpiStore))
+  if (desc->batch > 1 && (d.aux || d.epilogue != tlh::kEpiStore ||
+                          (d.residual && !d.sum_batches)))
     return int(hipErrorInvalidValue);
   return tlh::gemm_launch(d, stream);
 }

@@ -170,8 +170,26 @@ tlh_gemm_desc wgrad(const float *x, const float *dy, float *dw, float *db, int i
   return d;
 }
 
+// The three Q/K/V products of a layer as one batched descriptor: entry j
+// uses plane j of the activations (stride `act`) and the j-th of wq, wk, wv
+// in the parameter or gradient buffer (stride `weights`; each bias sits at
+// the same stride after its weight).
+void qkv_batch(tlh_gemm_desc &d, uint32_t act, ptrdiff_t weights) {
+  d.batch = 3;
+  if (d.trans_a) { // weight gradient: A = activations shared, B = dq/dk/dv planes
+    d.batch_stride_a = 0;
+    d.batch_stride_b = act;
+    d.batch_stride_c = uint32_t(weights);
+  } else { // dX: A = dq/dk/dv planes, B = the weights
+    d.batch_stride_a = act;
+    d.batch_stride_b = uint32_t(weights);
+    d.batch_stride_c = 0;
+  }
+  d.bias_batch_stride = uint32_t(weights);
+}
+
 int gemm(Program &p, tlh_gemm_desc d) {
-  if (d.trans_a) d.workspace = p.workspace; // tall-K weight gradients may split K
+  if (d.trans_a || d.sum_batches) d.workspace = p.workspace; // tall-K products may split K
   if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k * (d.batch > 1 ? d.batch : 1);
   return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, p.stream); });
 }
@@ -268,12 +286,19 @@ int backward(Program &p) {
                                     p.dq, p.dk, p.dv, c.batch, c.heads, c.seq, kHeadDim,
                                     1.0f / std::sqrt(float(kHeadDim)), 1, 1, 1, p.stream);
     }));
-    float *dqkv[3] = {p.dq, p.dk, p.dv};
-    for (int j = 0; j < 3; ++j)
-      TRY(gemm(p, wgrad(p.n1[l], dqkv[j], p.G(w + 2 * j), p.G(w + 2 * j + 1), D, D, R)));
-    for (int j = 0; j < 3; ++j) {
-      tlh_gemm_desc d = desc(dqkv[j], p.P(w + 2 * j), p.tmp, R, D, D, false, true);
-      d.beta = j == 0 ? 0.0f : 1.0f;
+    // dWq, dWk, dWv (+ bias gradients) as one batched product over the
+    // consecutive dq, dk, dv planes; dX = dq.Wq^T + dk.Wk^T + dv.Wv^T as one
+    // product whose K range runs through the three (dq_j, W_j) pairs.
+    {
+      tlh_gemm_desc d = wgrad(p.n1[l], p.dq, p.G(w), p.G(w + 1), D, D, R);
+      qkv_batch(d, uint32_t(p.dk - p.dq), p.G(w + 2) - p.G(w));
+      TRY(gemm(p, d));
+    }
+    {
+      tlh_gemm_desc d = desc(p.dq, p.P(w), p.tmp, R, D, D, false, true);
+      qkv_batch(d, uint32_t(p.dk - p.dq), p.P(w + 2) - p.P(w));
+      d.batch_stride_c = 0;
+      d.sum_batches = 1;
       TRY(gemm(p, d));
     }
     TRY(tlh_rms_norm_backward(p.tmp, p.x[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps, 1.0f,
@@ -397,16 +422,27 @@ int create(Program &p) {
   TRY(allocf(p, &p.dx, R * D));
   TRY(allocf(p, &p.tmp, R * D));
   TRY(allocf(p, &p.dgf, R * F));
-  TRY(allocf(p, &p.dq, R * D));
-  TRY(allocf(p, &p.dk, R * D));
-  TRY(allocf(p, &p.dv, R * D));
+  // dq, dk, dv: consecutive planes (the batched Q/K/V backward products)
+  TRY(allocf(p, &p.dq, 3 * R * D));
+  p.dk = p.dq + R * D;
+  p.dv = p.dq + 2 * R * D;
   TRY(allocf(p, &p.delta, B * H * T));
   // split-K workspace: the largest any weight-gradient GEMM asks for
   size_t ws = 0;
   const int shapes[4][2] = {{int(D), int(V)}, {int(F), int(D)}, {int(D), int(F)},
                             {int(D), int(D)}};
-  for (auto &s : shapes) {
-    tlh_gemm_desc d = desc(nullptr, nullptr, nullptr, s[0], s[1], int(R), true, false);
+  std::vector<tlh_gemm_desc> uses;
+  for (auto &s : shapes) uses.push_back(desc(nullptr, nullptr, nullptr, s[0], s[1], int(R), true, false));
+  {
+    tlh_gemm_desc d = desc(nullptr, nullptr, nullptr, int(D), int(D), int(R), true, false);
+    qkv_batch(d, uint32_t(R * D), ptrdiff_t(D * D + D));
+    uses.push_back(d);
+    d = desc(nullptr, nullptr, nullptr, int(R), int(D), int(D), false, true);
+    qkv_batch(d, uint32_t(R * D), ptrdiff_t(D * D + D));
+    d.sum_batches = 1;
+    uses.push_back(d);
+  }
+  for (auto &d : uses) {
     size_t e = 0;
     tlh_gemm_workspace_size(&d, &e);
     if (e > ws) ws = e;

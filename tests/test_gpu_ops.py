@@ -13,7 +13,7 @@ import torch
 
 import oracle_lib as O
 from gpu_util import Gpu, assert_close, assert_rel, rel_err, u32
-from templit_amd.native import EPI_GELU, EPI_GELU_BWD, GemmDesc
+from templit_amd.native import EPI_GELU, EPI_GELU_BWD, GemmDesc, check
 
 pytestmark = pytest.mark.gpu
 
@@ -246,6 +246,68 @@ def test_gemm_gelu_and_gelu_backward(g):
     out2, _ = gemm(g, dy, w, tb=True, epi=EPI_GELU_BWD, aux=uu)
     expect = O.binary("hadamard", O.matmul(dy, w.T), O.unary("gelu_derivative", uu))
     assert_rel(out2.reshape(M, N), expect, 1e-3)
+
+
+def _batched_desc(a, b, c, ta, tb, M, N, K, batch, sa, sb, sc):
+    d = GemmDesc()
+    d.a, d.b, d.c = a.data_ptr(), b.data_ptr(), c.data_ptr()
+    d.m, d.n, d.k = M, N, K
+    d.lda, d.ldb, d.ldc = (M if ta else K), (K if tb else N), N
+    d.trans_a, d.trans_b = int(ta), int(tb)
+    d.batch, d.batch_stride_a, d.batch_stride_b, d.batch_stride_c = batch, sa, sb, sc
+    return d
+
+
+def _with_workspace(g, keep, d):
+    n = ctypes.c_size_t()
+    check(g.lib.tlh_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)), "ws")
+    if n.value:
+        ws = g.empty((n.value,))
+        keep.append(ws)
+        d.workspace = ws.data_ptr()
+
+
+@pytest.mark.parametrize("K", [6144, 96])
+def test_gemm_batched_weight_grads_with_bias_grads(g, K):
+    # dW_j = X^T.dY_j and db_j = column sums of dY_j for three dY planes, one
+    # launch (the Q/K/V weight gradients), with split-K when K is long
+    M = N = 128
+    x = O.normal((K, M), 140, 0, 0.5)
+    dys = O.normal((3, K, N), 141, 0, 0.5)
+    gap = M * N + N + 64  # weight, bias and padding of one entry
+    out = np.zeros(3 * gap, np.float32)
+    keep = []
+    dx_, ddy, dout = g.dev(x), g.dev(dys), g.dev(out)
+    d = _batched_desc(dx_, ddy, dout, True, False, M, N, K, 3, 0, K * N, gap)
+    d.bias_grad = dout.data_ptr() + 4 * M * N
+    d.bias_batch_stride = gap
+    _with_workspace(g, keep, d)
+    g.call("tlh_gemm", ctypes.byref(d))
+    got = g.host(dout)
+    for j in range(3):
+        w = got[j * gap:j * gap + M * N].reshape(M, N)
+        bg = got[j * gap + M * N:j * gap + M * N + N]
+        assert_rel(w, O.matmul(x.T, dys[j]), 1e-3, f"dW[{j}]")
+        assert_close(bg, O.sum_to_shape(dys[j], [N]), rtol=1e-4, atol=1e-3, what=f"db[{j}]")
+
+
+@pytest.mark.parametrize("M,N,K", [(6144, 384, 384), (100, 70, 64)])
+def test_gemm_summed_batches(g, M, N, K):
+    # C = beta*C0 + residual + bias + sum_j A_j.W_j^T (the Q/K/V input gradient)
+    a = O.normal((3, M, K), 142, 0, 0.5)
+    w = O.normal((3, N, K), 143, 0, 0.5)
+    c0, res, bias = O.normal((M, N), 144), O.normal((M, N), 145), O.normal((N,), 146)
+    keep = []
+    da, dw, dc = g.dev(a), g.dev(w), g.dev(c0)
+    d = _batched_desc(da, dw, dc, False, True, M, N, K, 3, M * K, N * K, 0)
+    d.sum_batches = 1
+    d.beta = 1.0
+    dres, dbias = g.dev(res), g.dev(bias)
+    d.residual, d.bias = dres.data_ptr(), dbias.data_ptr()
+    _with_workspace(g, keep, d)
+    g.call("tlh_gemm", ctypes.byref(d))
+    expect = sum(O.matmul(a[j], w[j].T) for j in range(3)) + c0 + res + bias
+    assert_rel(g.host(dc).reshape(M, N), expect, 1e-3, "summed")
 
 
 def test_gemm_head_remap(g):
