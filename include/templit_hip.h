@@ -94,6 +94,10 @@ int tlh_event_record(void *event, void *stream);
 int tlh_event_synchronize(void *event);
 int tlh_event_elapsed_ms(void *start, void *end, float *host_ms);
 int tlh_event_destroy(void *event);
+/* `stream` waits, on the device, for the work recorded in `event`: a fork or
+ * join between two streams (captured as a graph dependency while recording).
+ * No reference counterpart: the Metal runtime has one serial encoder. */
+int tlh_stream_wait_event(void *stream, void *event);
 
 /* Command-buffer record/commit as a hipGraph (runtime.cpp:290-309).
  * begin/end_capture: thread-local capture, instantiated on end. */

@@ -221,6 +221,10 @@ TLH_API int tlh_event_record(void *event, void *stream) {
   return int(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)));
 }
 
+TLH_API int tlh_stream_wait_event(void *stream, void *event) {
+  return int(hipStreamWaitEvent(as_stream(stream), static_cast<hipEvent_t>(event), 0));
+}
+
 TLH_API int tlh_event_synchronize(void *event) {
   return int(hipEventSynchronize(static_cast<hipEvent_t>(event)));
 }

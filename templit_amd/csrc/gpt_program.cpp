@@ -70,6 +70,14 @@ struct Program {
         *dv = nullptr, *delta = nullptr, *workspace = nullptr;
   size_t workspace_elems = 0;
 
+  // Weight gradients run on a second stream, concurrently with the chain of
+  // input gradients; fork/join events order the two (a recorded graph keeps
+  // them as dependencies). While profiling everything runs on `stream`, so
+  // kernel durations are measured in isolation.
+  void *side = nullptr;
+  float *workspace_side = nullptr;
+  std::vector<void *> sync; // 2 + 8 per layer, see backward()
+
   std::vector<void *> allocations;
   void *graph = nullptr;
 
@@ -188,10 +196,40 @@ void qkv_batch(tlh_gemm_desc &d, uint32_t act, ptrdiff_t weights) {
   d.bias_batch_stride = uint32_t(weights);
 }
 
-int gemm(Program &p, tlh_gemm_desc d) {
-  if (d.trans_a || d.sum_batches) d.workspace = p.workspace; // tall-K products may split K
+bool concurrent(const Program &p) { return p.side != nullptr && !p.profiling; }
+
+// The side stream continues from the main stream's current point.
+int fork(Program &p, void *ev) {
+  if (!concurrent(p)) return 0;
+  TRY(tlh_event_record(ev, p.stream));
+  return tlh_stream_wait_event(p.side, ev);
+}
+
+// The side stream's work so far completes before what the main stream queues next.
+int join(Program &p, void *ev) {
+  if (!concurrent(p)) return 0;
+  TRY(tlh_event_record(ev, p.side));
+  return tlh_stream_wait_event(p.stream, ev);
+}
+
+// Waits on the main stream for an event that join-style recording left on
+// the side stream earlier in the step.
+int after(Program &p, void *ev) {
+  if (!concurrent(p)) return 0;
+  return tlh_stream_wait_event(p.stream, ev);
+}
+
+int record_side(Program &p, void *ev) {
+  if (!concurrent(p)) return 0;
+  return tlh_event_record(ev, p.side);
+}
+
+int gemm(Program &p, tlh_gemm_desc d, bool side = false) {
+  const bool on_side = side && concurrent(p);
+  // tall-K products may split K; each stream has its own workspace
+  if (d.trans_a || d.sum_batches) d.workspace = on_side ? p.workspace_side : p.workspace;
   if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k * (d.batch > 1 ? d.batch : 1);
-  return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, p.stream); });
+  return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, on_side ? p.side : p.stream); });
 }
 
 // Forward over the first `seq` <= cfg.seq positions of every sequence (the
@@ -255,32 +293,48 @@ int forward(Program &p, uint32_t seq) {
   return gemm(p, d);
 }
 
+// Input gradients run on the main stream; each weight gradient forks to the
+// side stream as soon as its upstream gradient exists, and the main stream
+// waits for it only before overwriting that gradient's buffer: dx is updated
+// in place twice per block, dgf and dq/dk/dv are rewritten one block later.
 int backward(Program &p) {
   const tlg_config &c = p.cfg;
   const int R = int(p.R), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
   const uint32_t last = 2 + 12 * c.layers;
+  auto ev = [&](int l, int i) { return p.sync[2 + 8 * size_t(l) + size_t(i)]; };
   // vocab projection
-  TRY(gemm(p, wgrad(p.nf, p.dlogits, p.G(last), p.G(last + 1), D, V, R)));
+  TRY(fork(p, p.sync[0]));
+  TRY(gemm(p, wgrad(p.nf, p.dlogits, p.G(last), p.G(last + 1), D, V, R), true));
   TRY(gemm(p, desc(p.dlogits, p.P(last), p.tmp, R, D, V, false, true)));
   TRY(tlh_rms_norm_backward(p.tmp, p.x[c.layers], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
                             0.0f, p.stream));
   for (int l = int(c.layers) - 1; l >= 0; --l) {
     const uint32_t w = 2 + 12 * uint32_t(l);
+    const bool top = l + 1 == int(c.layers);
     // FFN: x[l+1] = x_mid + W2.GELU(W1.n2 + b1) + b2
-    TRY(gemm(p, wgrad(p.g[l], p.dx, p.G(w + 10), p.G(w + 11), F, D, R)));
+    TRY(fork(p, ev(l, 0)));
+    TRY(gemm(p, wgrad(p.g[l], p.dx, p.G(w + 10), p.G(w + 11), F, D, R), true));
+    TRY(record_side(p, ev(l, 1)));
+    if (!top) TRY(after(p, ev(l + 1, 3))); // the block above's dW1 has read dgf
     {
       tlh_gemm_desc d = desc(p.dx, p.P(w + 10), p.dgf, R, F, D, false, true);
       d.epilogue = TLH_EPI_GELU_BWD;
       d.aux = p.u[l];
       TRY(gemm(p, d));
     }
-    TRY(gemm(p, wgrad(p.n2[l], p.dgf, p.G(w + 8), p.G(w + 9), D, F, R)));
+    TRY(fork(p, ev(l, 2)));
+    TRY(gemm(p, wgrad(p.n2[l], p.dgf, p.G(w + 8), p.G(w + 9), D, F, R), true));
+    TRY(record_side(p, ev(l, 3)));
     TRY(gemm(p, desc(p.dgf, p.P(w + 8), p.tmp, R, D, F, false, true)));
+    TRY(after(p, ev(l, 1))); // dW2 has read dx
     TRY(tlh_rms_norm_backward(p.tmp, p.x_mid[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps,
                               1.0f, p.stream));
     // attention: x_mid = x + Wo.attn(n1) + bo
-    TRY(gemm(p, wgrad(p.o[l], p.dx, p.G(w + 6), p.G(w + 7), D, D, R)));
+    TRY(fork(p, ev(l, 4)));
+    TRY(gemm(p, wgrad(p.o[l], p.dx, p.G(w + 6), p.G(w + 7), D, D, R), true));
+    TRY(record_side(p, ev(l, 5)));
     TRY(gemm(p, desc(p.dx, p.P(w + 6), p.tmp, R, D, D, false, true)));
+    if (!top) TRY(after(p, ev(l + 1, 7))); // the block above's dWq/k/v have read dq/dk/dv
     TRY(timed(p, p.attn_spans, [&] {
       return tlh_attention_backward(p.q[l], p.k[l], p.v[l], p.o[l], p.tmp, p.lse[l], p.delta,
                                     p.dq, p.dk, p.dv, c.batch, c.heads, c.seq, kHeadDim,
@@ -289,11 +343,13 @@ int backward(Program &p) {
     // dWq, dWk, dWv (+ bias gradients) as one batched product over the
     // consecutive dq, dk, dv planes; dX = dq.Wq^T + dk.Wk^T + dv.Wv^T as one
     // product whose K range runs through the three (dq_j, W_j) pairs.
+    TRY(fork(p, ev(l, 6)));
     {
       tlh_gemm_desc d = wgrad(p.n1[l], p.dq, p.G(w), p.G(w + 1), D, D, R);
       qkv_batch(d, uint32_t(p.dk - p.dq), p.G(w + 2) - p.G(w));
-      TRY(gemm(p, d));
+      TRY(gemm(p, d, true));
     }
+    TRY(record_side(p, ev(l, 7)));
     {
       tlh_gemm_desc d = desc(p.dq, p.P(w), p.tmp, R, D, D, false, true);
       qkv_batch(d, uint32_t(p.dk - p.dq), p.P(w + 2) - p.P(w));
@@ -301,6 +357,7 @@ int backward(Program &p) {
       d.sum_batches = 1;
       TRY(gemm(p, d));
     }
+    TRY(after(p, ev(l, 5))); // dWo has read dx
     TRY(tlh_rms_norm_backward(p.tmp, p.x[l], nullptr, p.dx, nullptr, p.R, c.dim, kRmsEps, 1.0f,
                               p.stream));
   }
@@ -308,7 +365,8 @@ int backward(Program &p) {
   // as a column sum over the batch of the [B, T*D] view.
   TRY(tlh_fill_f32(p.G(0), 0.0f, p.size[0], p.stream));
   TRY(tlh_scatter_add_rows(p.dx, p.tokens, p.R, c.dim, p.G(0), c.vocab, p.stream));
-  return tlh_column_sum(p.dx, c.batch, c.seq * c.dim, p.G(1), 0.0f, p.stream);
+  TRY(tlh_column_sum(p.dx, c.batch, c.seq * c.dim, p.G(1), 0.0f, p.stream));
+  return join(p, p.sync[1]); // every weight gradient is complete
 }
 
 int optimizer_step(Program &p, float max_norm) {
@@ -456,7 +514,13 @@ int create(Program &p) {
         p.offset[w + 3] - p.offset[w + 1] != p.offset[w + 5] - p.offset[w + 3])
       return kInvalidValue;
   }
-  if (ws) TRY(allocf(p, &p.workspace, ws));
+  if (ws) {
+    TRY(allocf(p, &p.workspace, ws));
+    TRY(allocf(p, &p.workspace_side, ws));
+  }
+  TRY(tlh_stream_create(&p.side));
+  p.sync.resize(2 + 8 * L);
+  for (auto &e : p.sync) TRY(tlh_event_create(&e));
   p.lr = 1e-3f;
   TRY(write_scalars(p, 0.9f, 0.999f));
   return tlh_stream_synchronize(p.stream);
@@ -466,6 +530,11 @@ void release(Program &p) {
   if (p.graph) tlh_graph_destroy(p.graph);
   for (void *e : p.events) tlh_event_destroy(e);
   p.events.clear();
+  for (void *e : p.sync)
+    if (e) tlh_event_destroy(e);
+  p.sync.clear();
+  if (p.side) tlh_stream_destroy(p.side);
+  p.side = nullptr;
   for (void *a : p.allocations) tlh_free(a);
   p.allocations.clear();
 }

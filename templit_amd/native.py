@@ -69,6 +69,7 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_event_synchronize": [P],
     "tlh_event_elapsed_ms": [P, P, POINTER(c_float)],
     "tlh_event_destroy": [P],
+    "tlh_stream_wait_event": [P, P],
     "tlh_graph_begin_capture": [P],
     "tlh_graph_end_capture": [P, POINTER(c_void_p)],
     "tlh_graph_launch": [P, P],

@@ -154,6 +154,23 @@ def test_c4_graph_replay_matches_eager(c4):
         assert rel_l2(params, eager[step][1]) < 1e-6
 
 
+def test_c4_concurrent_weight_gradients_match_serial(c4):
+    # The weight gradients run on a second stream next to the input-gradient
+    # chain; the profiled step runs everything on one stream. Every kernel of
+    # the step is deterministic (no float atomics: the embedding scatter adds
+    # in index order), so a missing fork/join shows up as a bitwise difference.
+    runs = []
+    for step_fn in (c4.train_step, c4.profile_step):
+        c4.init_params(seed=1, std=0.02)
+        c4.set_optimizer(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+        for _ in range(2):
+            step_fn(1.0 / 6144, 1.0)
+        c4.synchronize()
+        runs.append((c4.losses(), c4.get_grads(), c4.get_params()))
+    for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
+        assert np.array_equal(got, want), what
+
+
 def test_c4_loss_decreases_on_a_fixed_batch(c4):
     c4.init_params(seed=3, std=0.02)
     c4.set_optimizer(lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)

@@ -537,14 +537,31 @@ def test_scatter_add_rows(g):
     ids = np.array([2, 0, 2, 1], np.uint32)
     dst = g.dev(base)
     g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), 4, 3, dst, 4)
-    np.testing.assert_allclose(g.host(dst), O.scatter_add_rows(base, ids, values), atol=1e-4)
-    V, D, n = 2048, 384, 6144
+    np.testing.assert_array_equal(g.host(dst), O.scatter_add_rows(base, ids, values))
+
+
+@pytest.mark.parametrize("V,D,n,skew", [
+    (2048, 384, 6144, None),      # the GPT token table
+    (2048, 1024, 8192, None),     # the scaled one
+    (50000, 64, 3000, None),      # several destination rows per block
+    (3, 13000, 2500, None),       # rows longer than one block's LDS: column chunks
+    (100, 7, 1, None), (100, 7, 1023, None), (100, 7, 1025, None),
+    (64, 33, 5000, "one"),        # every id the same row
+    (64, 33, 5000, "two"),        # two rows, interleaved
+])
+def test_scatter_add_rows_sequential_order(g, V, D, n, skew):
+    # Adds happen in increasing index order per element, without atomics:
+    # the result equals the sequential loop bit for bit.
     values = O.normal((n, D), 68)
     ids = O.uniform_u32((n,), 69, V)
-    dst = g.zeros((V, D))
+    if skew == "one":
+        ids[:] = 17
+    elif skew == "two":
+        ids = np.where(np.arange(n) % 3 == 0, 5, 60).astype(np.uint32)
+    base = O.normal((V, D), 72)
+    dst = g.dev(base)
     g.call("tlh_scatter_add_rows", g.dev(values), g.dev(ids), n, D, dst, V)
-    assert_close(g.host(dst), O.scatter_add_rows(np.zeros((V, D), np.float32), ids, values),
-                 rtol=1e-4, atol=1e-5)
+    np.testing.assert_array_equal(g.host(dst), O.scatter_add_rows(base, ids, values))
 
 
 # ---------------------------------------------------------------------------
