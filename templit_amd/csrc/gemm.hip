@@ -81,6 +81,113 @@ __device__ inline void epilogue_store(const GemmParams &p, const float *bias, fl
   C[idx] = v;
 }
 
+// One block's output tile, K range and operand bases.
+struct BlockCtx {
+  int tm, m0, n0;
+  int k_begin, k_end;
+  const float *A, *B;
+  float *C;
+  const float *bias;
+  float *bias_grad;
+};
+
+template <int BM, int BN>
+__device__ inline BlockCtx block_ctx(const GemmParams &p) {
+  BlockCtx b;
+  // Blocks are dispatched round-robin over the 8 XCDs (block x runs on XCD
+  // x % 8), each with its own L2. Give XCD j the contiguous tile range
+  // [j*G/8, (j+1)*G/8): tiles of the same tile row then share their A rows
+  // (and neighbouring rows their B columns) in one L2.
+  const int nblk = int(gridDim.x);
+  const int tile = (p.xcd_remap && (nblk & 7) == 0)
+                       ? int(blockIdx.x & 7) * (nblk >> 3) + int(blockIdx.x >> 3)
+                       : int(blockIdx.x);
+  b.tm = tile / p.tiles_n;
+  b.m0 = b.tm * BM;
+  b.n0 = (tile - b.tm * p.tiles_n) * BN;
+  // (p stays unmodified: writing a kernel-argument struct that is also
+  // passed by reference moves it to scratch memory)
+  b.A = p.A;
+  b.B = p.B;
+  b.C = p.C;
+  b.bias = p.bias;
+  b.bias_grad = p.bias_grad;
+  // blockIdx.z = output entry * splits + split (a split is a K range).
+  const int zs = p.splits > 1 ? int(blockIdx.z) % p.splits : 0;
+  const int zb = p.splits > 1 ? int(blockIdx.z) / p.splits : int(blockIdx.z);
+  b.k_begin = 0;
+  b.k_end = p.K;
+  if (p.batch_ndim > 0) {
+    uint32_t rem = uint32_t(zb);
+    size_t oa = 0, ob = 0, oc = 0;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+      const uint32_t c = rem % p.batch_shape[d];
+      rem /= p.batch_shape[d];
+      oa += size_t(c) * p.bsa[d];
+      ob += size_t(c) * p.bsb[d];
+      oc += size_t(c) * p.bsc[d];
+    }
+    b.A += oa;
+    b.B += ob;
+    b.C += oc;
+    if (b.bias) b.bias += size_t(zb) * p.bias_bstride;
+    if (b.bias_grad) b.bias_grad += size_t(zb) * p.bias_bstride;
+  }
+  if (p.splits > 1) {
+    b.k_begin = zs * p.k_chunk;
+    b.k_end = min(p.K, b.k_begin + p.k_chunk);
+    b.C = p.workspace + (size_t(zb) * p.splits + zs) * p.M * p.N;
+  }
+  return b;
+}
+
+// Bias gradient of the blocks of the first tile row: each thread's partial
+// column sum goes through LDS (free again: every thread is past the main
+// loop's last barrier), then to the output or the split-K partials.
+template <int BN>
+__device__ inline void bias_grad_store(const GemmParams &p, const BlockCtx &b, float *smem,
+                                       float bsum, bool full) {
+  constexpr int BGROUPS = 256 / BN;
+  const int tid = threadIdx.x;
+  smem[tid] = bsum;
+  __syncthreads();
+  const int n = b.n0 + tid;
+  if (tid < BN && (full || n < p.N)) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < BGROUPS; ++g) t += smem[g * BN + tid];
+    if (p.splits > 1) {
+      p.workspace[size_t(p.batch) * p.splits * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
+    } else {
+      b.bias_grad[n] = p.beta != 0.0f ? t + p.beta * b.bias_grad[n] : t;
+    }
+  }
+}
+
+// Writes the accumulators of one wave (TM x TN 32x32 tiles) through the epilogue.
+template <int TM, int TN, int WM, int WN, bool FULL>
+__device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f16x (&acc)[TM][TN],
+                                 int wm, int wn, int r, int hk) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = b.n0 + wn * WN + j * 32 + r;
+      if (!FULL && n >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = b.m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
+        if (!FULL && m >= p.M) continue;
+        if (p.splits > 1) {
+          b.C[size_t(m) * p.N + n] = acc[i][j][v];
+        } else {
+          epilogue_store(p, b.bias, b.C, m, n, acc[i][j][v]);
+        }
+      }
+    }
+  }
+}
+
 // FULL: M, N are multiples of the tile, the K range of every block is a
 // multiple of BK and the operands are float4-aligned: no bounds checks.
 template <int BM, int BN, int WM, int WN, int BK, bool TA, bool TB, bool VEC, bool FULL>
@@ -110,51 +217,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int r = lane & 31;
   const int hk = lane >> 5;
 
-  // Blocks are dispatched round-robin over the 8 XCDs (block x runs on XCD
-  // x % 8), each with its own L2. Give XCD j the contiguous tile range
-  // [j*G/8, (j+1)*G/8): tiles of the same tile row then share their A rows
-  // (and neighbouring rows their B columns) in one L2.
-  const int nblk = int(gridDim.x);
-  const int tile = (p.xcd_remap && (nblk & 7) == 0)
-                       ? int(blockIdx.x & 7) * (nblk >> 3) + int(blockIdx.x >> 3)
-                       : int(blockIdx.x);
-  const int tm = tile / p.tiles_n;
-  const int tn = tile - tm * p.tiles_n;
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
-
-  // (p stays unmodified: writing a kernel-argument struct that is also
-  // passed by reference moves it to scratch memory)
-  const float *A = p.A;
-  const float *B = p.B;
-  float *C = p.C;
-  const float *bias = p.bias;
-  // blockIdx.z = output entry * splits + split (a split is a K range).
-  const int zs = p.splits > 1 ? int(blockIdx.z) % p.splits : 0;
-  const int zb = p.splits > 1 ? int(blockIdx.z) / p.splits : int(blockIdx.z);
-  float *bias_grad = p.bias_grad;
-  int k_begin = 0, k_end = p.K;
-  if (p.batch_ndim > 0) {
-    uint32_t rem = uint32_t(zb);
-    size_t oa = 0, ob = 0, oc = 0;
-    for (int d = p.batch_ndim - 1; d >= 0; --d) {
-      const uint32_t c = rem % p.batch_shape[d];
-      rem /= p.batch_shape[d];
-      oa += size_t(c) * p.bsa[d];
-      ob += size_t(c) * p.bsb[d];
-      oc += size_t(c) * p.bsc[d];
-    }
-    A += oa;
-    B += ob;
-    C += oc;
-    if (bias) bias += size_t(zb) * p.bias_bstride;
-    if (bias_grad) bias_grad += size_t(zb) * p.bias_bstride;
-  }
-  if (p.splits > 1) {
-    k_begin = zs * p.k_chunk;
-    k_end = min(p.K, k_begin + p.k_chunk);
-    C = p.workspace + (size_t(zb) * p.splits + zs) * p.M * p.N;
-  }
+  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const int tm = ctx.tm, m0 = ctx.m0, n0 = ctx.n0;
+  const int k_begin = ctx.k_begin, k_end = ctx.k_end;
+  const float *A = ctx.A;
+  const float *B = ctx.B;
 
   // ---- global -> register prefetch ----------------------------------------
   f4 ra[A_CHUNKS], rb[B_CHUNKS];
@@ -326,41 +393,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       __syncthreads();
     }
   }
-  if (do_bias) { // every thread is past the loop's last barrier: smem is free
-    smem[tid] = bsum;
-    __syncthreads();
-    const int n = n0 + tid;
-    if (tid < BN && n < p.N) {
-      float t = 0.f;
-#pragma unroll
-      for (int g = 0; g < BGROUPS; ++g) t += smem[g * BN + tid];
-      if (p.splits > 1) {
-        p.workspace[size_t(p.batch) * p.splits * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
-      } else {
-        bias_grad[n] = p.beta != 0.0f ? t + p.beta * bias_grad[n] : t;
-      }
-    }
-  }
-
-  // ---- epilogue --------------------------------------------------------------
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * WN + j * 32 + r;
-      if (!FULL && n >= p.N) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
-        if (!FULL && m >= p.M) continue;
-        if (p.splits > 1) {
-          C[size_t(m) * p.N + n] = acc[i][j][v];
-        } else {
-          epilogue_store(p, bias, C, m, n, acc[i][j][v]);
-        }
-      }
-    }
-  }
+  if (do_bias) bias_grad_store<BN>(p, ctx, smem, bsum, FULL);
+  store_acc<TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
 }
 
 // Sums the split-K partials of every output entry in split order --

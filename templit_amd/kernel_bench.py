@@ -24,7 +24,9 @@ GEMM_SHAPES = [  # name, M, N, K, trans_a, trans_b, bias gradient
     ("dN f->d", R, D, F, 0, 1, 0), ("dX vocab", R, D, V, 0, 1, 0),
     ("wgrad dd", D, D, R, 1, 0, 1), ("wgrad fd", F, D, R, 1, 0, 1),
     ("wgrad df", D, F, R, 1, 0, 1), ("wgrad dv", D, V, R, 1, 0, 1),
+    ("d1024 up", 8192, 4096, 1024, 0, 0, 0), ("d1024 sq", 8192, 1024, 1024, 0, 0, 0),
 ]
+BUF = 8192 * 4096  # largest operand of the shapes above
 ATTENTION_SHAPES = [(32, 6, 192), (8, 16, 1024)]  # (B, H, T), head dim 64
 
 
@@ -68,10 +70,10 @@ class Bench:
         self.hip.tlh_stream_destroy(self.stream)
 
 
-def run_gemm(b: Bench, iters: int, sweep: bool) -> None:
-    a = b.alloc(R * V, 1)
-    bb = b.alloc(R * V, 2)
-    c = b.alloc(R * V)
+def run_gemm(b: Bench, iters: int, sweep: bool, only: str | None = None) -> None:
+    a = b.alloc(BUF, 1)
+    bb = b.alloc(BUF, 2)
+    c = b.alloc(BUF)
     bias_grad = b.alloc(V)
     ws_elems = 16 * (F * V + V)
     ws = b.alloc(ws_elems)
@@ -80,6 +82,8 @@ def run_gemm(b: Bench, iters: int, sweep: bool) -> None:
         plans += [(bm, bn, s, bk) for bk in (16, 32) for bm in (64, 128) for bn in (64, 128)
                   for s in (1, 4, 8, 16)]
     for name, M, N, K, ta, tb, bgrad in GEMM_SHAPES:
+        if only and only not in name:
+            continue
         d = GemmDesc()
         d.a, d.b, d.c = a, bb, c
         d.m, d.n, d.k = M, N, K
@@ -140,13 +144,14 @@ def main() -> int:
     ap.add_argument("--attention", action="store_true")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--only", help="GEMM shapes whose name contains this text")
     args = ap.parse_args()
     if not (args.gemm or args.attention):
         args.gemm = args.attention = True
     b = Bench()
     try:
         if args.gemm:
-            run_gemm(b, args.iters, args.sweep)
+            run_gemm(b, args.iters, args.sweep, args.only)
         if args.attention:
             run_attention(b, args.iters)
     finally:

@@ -222,6 +222,36 @@ def test_gemm_weight_grad_fused_bias_grad(g, M, N, K, split, beta):
     assert_close(db, O.sum_to_shape(dy, [N]) + beta * b0, rtol=1e-4, atol=1e-3, what="db")
 
 
+@pytest.fixture
+def forced_plan(g):
+    """tlh_gemm_set_plan is process-wide: restore the planner afterwards."""
+    yield lambda *plan: check(g.lib.tlh_gemm_set_plan(*plan), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, 16), "set_plan")
+
+
+@pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
+@pytest.mark.parametrize("bk", [16, 32])
+def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
+    # Every tile / K-tile plan on a tile-aligned shape (the bounds-free
+    # path), every operand layout, and the weight-gradient form with its
+    # bias gradient, unsplit and split over K.
+    M, N, K = 256, 384, 512
+    for ta in (False, True):
+        for tb in (False, True):
+            forced_plan(bm, bn, 1, bk)
+            a = O.normal((K, M) if ta else (M, K), 150, 0, 0.5)
+            b = O.normal((N, K) if tb else (K, N), 151, 0, 0.5)
+            out, _ = gemm(g, a, b, ta, tb)
+            expect = O.matmul(a.T if ta else a, b.T if tb else b)
+            assert_rel(out.reshape(M, N), expect, 1e-3, f"gemm ta={ta} tb={tb}")
+    x, dy = O.normal((K, M), 152, 0, 0.5), O.normal((K, N), 153, 0, 0.5)
+    for splits in (1, 4):
+        forced_plan(bm, bn, splits, bk)
+        dw, db = gemm(g, x, dy, ta=True, bias_grad_init=np.zeros(N, np.float32))
+        assert_rel(dw.reshape(M, N), O.matmul(x.T, dy), 1e-3, f"dW splits={splits}")
+        assert_close(db, O.sum_to_shape(dy, [N]), rtol=1e-4, atol=1e-3, what="db")
+
+
 def test_gemm_bias_residual_beta(g):
     M, N, K = 1000, 384, 384
     a, b = O.normal((M, K), 14, 0, 0.1), O.normal((K, N), 15, 0, 0.1)
