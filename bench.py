@@ -82,6 +82,153 @@ def gemm_d1024(hip, stream) -> dict:
             hip.tlh_free(b)
 
 
+class DeviceTimer:
+    """Device buffers and HIP-event timing on one stream, for the kernel
+    configurations below."""
+
+    def __init__(self, hip, stream):
+        from templit_amd.native import check
+
+        self.hip, self.stream, self.check = hip, stream, check
+        self.bufs = []
+        self.ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+        for e in self.ev:
+            check(hip.tlh_event_create(ctypes.byref(e)), "event")
+
+    def buf(self, n, seed=None, mean=0.0, std=1.0, bound=None):
+        ptr = ctypes.c_void_p()
+        self.check(self.hip.tlh_malloc(ctypes.byref(ptr), max(n, 1) * 4), "malloc")
+        self.bufs.append(ptr.value)
+        if bound is not None:
+            self.check(self.hip.tlh_fill_uniform_u32(ptr.value, n, seed, bound, self.stream), "fill")
+        elif seed is not None:
+            self.check(self.hip.tlh_fill_normal(ptr.value, n, seed, mean, std, self.stream), "fill")
+        return ptr.value
+
+    def us(self, fn, iters=50):
+        for _ in range(3):
+            fn()
+        self.check(self.hip.tlh_event_record(self.ev[0], self.stream), "record")
+        for _ in range(iters):
+            fn()
+        self.check(self.hip.tlh_event_record(self.ev[1], self.stream), "record")
+        self.check(self.hip.tlh_stream_synchronize(self.stream), "sync")
+        ms = ctypes.c_float()
+        self.check(self.hip.tlh_event_elapsed_ms(self.ev[0], self.ev[1], ctypes.byref(ms)),
+                   "elapsed")
+        return ms.value * 1e3 / iters
+
+    def close(self):
+        for b in self.bufs:
+            self.hip.tlh_free(b)
+        for e in self.ev:
+            self.hip.tlh_event_destroy(e)
+
+
+# Row-op sizes: X [6144,384], H [6144,1536], logits [6144,2048]
+R2, D2, F2, V2 = 6144, 384, 1536, 2048
+# Minimum HBM bytes per launch (each operand read once, each result written once)
+ROW_OP_BYTES = {
+    "rmsnorm_fwd": 4 * (2 * R2 * D2 + D2), "rmsnorm_bwd": 4 * (3 * R2 * D2 + D2),
+    "gelu_fwd": 4 * 2 * R2 * F2, "gelu_bwd": 4 * 3 * R2 * F2,
+    "softmax_fwd": 4 * 2 * R2 * V2, "softmax_bwd": 4 * 3 * R2 * V2,
+    "cross_entropy_fwd": 4 * (R2 * V2 + 2 * R2),
+    "cross_entropy_bwd_scaled": 4 * (2 * R2 * V2 + 2 * R2),
+}
+C1 = (768, 384, 1536)           # A [768,384] . B [384,1536] + bias [1,1536]
+C3 = (32, 6, 192, 64)           # attention Q, K, V, dO [B, H, T, 64], causal
+
+
+def kernel_configs(hip, stream) -> dict:
+    """The single-kernel configurations, each against its roofline:
+    matmul + bias (fp32 MFMA), the row ops (HBM) and causal attention
+    (fp32 MFMA, causal-effective flops)."""
+    from templit_amd.native import GemmDesc, u32_array
+
+    t = DeviceTimer(hip, stream)
+    ck, s = t.check, stream
+    out: dict = {}
+    try:
+        # c1: through the runtime's two calls (mult, then the broadcast add of
+        # nn::Layer, execute.h:241-252) and as one GEMM with the bias fused
+        M, K, N = C1
+        a, b, bias, c = t.buf(M * K, 1, 0, 0.02), t.buf(K * N, 2, 0, 0.02), t.buf(N, 3, 0, 0.02), t.buf(M * N)
+        shape, sa, sb = u32_array([M, N]), u32_array([N, 1]), u32_array([0, 1])
+        flops = 2.0 * M * N * K + M * N
+
+        def mult_add():
+            ck(hip.tlh_matmul(a, b, c, M, K, N, K, 1, N, 1, N, 1, 0, None, None, None, None, s),
+               "matmul")
+            ck(hip.tlh_add(c, bias, c, 2, shape, sa, sb, s), "add")
+
+        d = GemmDesc()
+        d.a, d.b, d.c, d.bias = a, b, c, bias
+        d.m, d.n, d.k = M, N, K
+        d.lda, d.ldb, d.ldc = K, N, N
+        rows = {}
+        for name, fn in (("mult_then_add", mult_add),
+                         ("fused_bias_gemm", lambda: ck(hip.tlh_gemm(ctypes.byref(d), s), "gemm"))):
+            us = t.us(fn)
+            tf = flops / us / 1e6
+            rows[name] = {"us": round(us, 2), "tflops": round(tf, 2),
+                          "frac": round(tf / FP32_MFMA_PEAK, 4)}
+        out["matmul_bias_768x384x1536"] = {"bound": "mfma", "flops": flops, **rows}
+
+        # c2: row ops at the GPT shapes
+        x, gx, gain = t.buf(R2 * D2, 4), t.buf(R2 * D2, 5), t.buf(D2, 6, 1.0, 0.02)
+        y = t.buf(R2 * D2)
+        h, gh, hy = t.buf(R2 * F2, 7), t.buf(R2 * F2, 8), t.buf(R2 * F2)
+        lg, glg, ly = t.buf(R2 * V2, 9), t.buf(R2 * V2, 10), t.buf(R2 * V2)
+        tgt, loss, scale = t.buf(R2, 11, bound=V2), t.buf(R2), t.buf(R2, 12)
+        eps = 1e-6
+        ops = {
+            "rmsnorm_fwd": lambda: hip.tlh_rms_norm(x, gain, y, None, R2, D2, eps, s),
+            "rmsnorm_bwd": lambda: hip.tlh_rms_norm_backward(gx, x, gain, y, None, R2, D2, eps,
+                                                             0.0, s),
+            "gelu_fwd": lambda: hip.tlh_gelu(h, hy, R2 * F2, s),
+            "gelu_bwd": lambda: hip.tlh_gelu_backward(gh, h, hy, R2 * F2, s),
+            "softmax_fwd": lambda: hip.tlh_softmax(lg, ly, R2, V2, s),
+            "softmax_bwd": lambda: hip.tlh_softmax_backward(glg, ly, glg, R2, V2, s),
+            "cross_entropy_fwd": lambda: hip.tlh_cross_entropy_rows(lg, tgt, loss, R2, V2, s),
+            "cross_entropy_bwd_scaled": lambda: hip.tlh_cross_entropy_rows_backward(
+                lg, tgt, ly, R2, V2, scale, s),
+        }
+        rowops = {}
+        for name, fn in ops.items():
+            us = t.us(lambda: ck(fn(), name))
+            gbs = ROW_OP_BYTES[name] / us / 1e3
+            rowops[name] = {"us": round(us, 2), "bytes": ROW_OP_BYTES[name],
+                            "gb_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 4)}
+        out["row_ops"] = {"bound": "hbm", "peak_gb_s": HBM_PEAK, **rowops}
+
+        # c3: fused causal attention
+        B, H, T, Dh = C3
+        n = B * H * T * Dh
+        q, k, v = (t.buf(n, 13 + i, 0.0, 0.125) for i in range(3))
+        do = t.buf(n, 16)
+        o, dq, dk, dv = (t.buf(n) for _ in range(4))
+        lse, delta = t.buf(B * H * T), t.buf(B * H * T)
+        sc = 1.0 / 8.0
+        fwd = lambda: ck(hip.tlh_attention_forward(q, k, v, o, lse, B, H, T, Dh, sc, 1, 0, s),
+                         "attention forward")
+        bwd = lambda: ck(hip.tlh_attention_backward(q, k, v, o, do, lse, delta, dq, dk, dv, B,
+                                                    H, T, Dh, sc, 1, 0, 0, s),
+                         "attention backward")
+        fwd()
+        att = {}
+        for name, fn, mult in (("forward", fwd, 4), ("backward", bwd, 10)):
+            us = t.us(fn)
+            causal = mult * B * H * T * T * Dh / 2
+            tf = causal / us / 1e6
+            att[name] = {"us": round(us, 2), "causal_flops": causal, "tflops": round(tf, 2),
+                         "frac": round(tf / FP32_MFMA_PEAK, 4)}
+        out["attention_b32_h6_t192"] = {"bound": "mfma", **att}
+    finally:
+        t.close()
+    log(f"[bench] kernel configurations: {json.dumps(out)}")
+    return out
+
+
 SCALED = dict(vocab=2048, seq=1024, dim=1024, heads=16, layers=12, batch=8)
 EOS = 256  # the BPE tokeniser's end-of-sequence id (dataset/ tokens split on it)
 
@@ -200,7 +347,57 @@ def cpu_baseline(sample_batch: int, steps: int) -> dict:
     return {"value": round(rows * steps / dt, 2), "unit": "tokens/s", "cores": 1,
             "kind": "port",
             "sample": f"{steps} oracle training steps of the same model at batch "
-                      f"{sample_batch} ({rows} tokens/step, {dt:.1f} s), single thread"}
+                      f"{sample_batch} ({rows} tokens/step, {dt:.1f} s), single thread",
+            "kernel_configs": cpu_kernel_configs()}
+
+
+def cpu_kernel_configs() -> dict:
+    """The oracle (one thread) on the kernel configurations, full size."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    out = {}
+    M, K, N = C1
+    a, b, bias = O.normal((M, K), 1, 0, 0.02), O.normal((K, N), 2, 0, 0.02), O.normal((1, N), 3)
+    dt = timed(lambda: O.binary("add", O.matmul(a, b), bias))
+    out["matmul_bias_768x384x1536"] = {"s": round(dt, 3),
+                                       "gflops": round((2.0 * M * N * K + M * N) / dt / 1e9, 2)}
+    x, gx, gain = O.normal((R2, D2), 4), O.normal((R2, D2), 5), O.normal((D2,), 6, 1.0, 0.02)
+    h, gh = O.normal((R2, F2), 7), O.normal((R2, F2), 8)
+    lg, glg = O.normal((R2, V2), 9), O.normal((R2, V2), 10)
+    tgt = O.uniform_u32((R2,), 11, V2)
+    y = O.softmax(lg)
+    ops = {
+        "rmsnorm_fwd": lambda: O.rms_norm(x, gain),
+        "rmsnorm_bwd": lambda: O.rms_norm_backward(gx, x, gain),
+        "gelu_fwd": lambda: O.unary("gelu", h),
+        "gelu_bwd": lambda: O.binary("hadamard", gh, O.unary("gelu_derivative", h)),
+        "softmax_fwd": lambda: O.softmax(lg),
+        "softmax_bwd": lambda: O.softmax_backward(glg, y),
+        "cross_entropy_fwd": lambda: O.cross_entropy(lg, tgt),
+        "cross_entropy_bwd_scaled": lambda: O.cross_entropy_backward(lg, tgt),
+    }
+    rowops = {}
+    for name, fn in ops.items():
+        dt = timed(fn)
+        rowops[name] = {"s": round(dt, 4), "gb_s": round(ROW_OP_BYTES[name] / dt / 1e9, 2)}
+    out["row_ops"] = rowops
+    B, H, T, Dh = C3
+    q, k, v = (O.normal((B, H, T, Dh), 13 + i, 0.0, 0.125) for i in range(3))
+    do = O.normal((B, H, T, Dh), 16)
+    t0 = time.perf_counter()
+    o, probs = O.attention_forward(q, k, v)
+    t1 = time.perf_counter()
+    O.attention_backward(q, k, v, probs, do)
+    t2 = time.perf_counter()
+    out["attention_b32_h6_t192"] = {"forward_s": round(t1 - t0, 3), "backward_s": round(t2 - t1, 3)}
+    log(f"[bench] CPU oracle kernel configurations: {json.dumps(out)}")
+    return out
 
 
 def main() -> int:
@@ -214,6 +411,8 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="time eager steps instead of hipGraph replays (for counter runs)")
     ap.add_argument("--skip-d1024", action="store_true")
+    ap.add_argument("--skip-kernels", action="store_true",
+                    help="skip the single-kernel configurations (matmul+bias, row ops, attention)")
     ap.add_argument("--skip-scaled", action="store_true",
                     help="skip the d=1024 / 12-block / T=1024 configuration")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -260,10 +459,13 @@ def main() -> int:
         f"{tok_s:.0f} tokens/s, loss {loss:.4f}")
 
     prof = prog.profile_step(root, MAX_NORM)
-    gemm_tflops = prof["gemm_flops"] / (prof["gemm_ms"] * 1e-3) / 1e12
+    # kernel time: each GEMM launch of that step again, 10 times back to back
+    gemm_ms = prog.time_gemms(10)
+    gemm_tflops = prof["gemm_flops"] / (gemm_ms * 1e-3) / 1e12
     log(f"[bench] profiled step: {prof}")
     d1024 = None if args.skip_d1024 else gemm_d1024(hip, prog.stream)
     log(f"[bench] d=1024 GEMM: {d1024}")
+    kernels = None if args.skip_kernels else kernel_configs(hip, prog.stream)
     prog.close()
 
     result = {
@@ -296,15 +498,19 @@ def main() -> int:
             "traffic": gemm_traffic(),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, "
                             "profiles/gpt_step_b32_t192_d384_gemm_hbm_traffic.md)",
-            "algorithmic_bytes_per_launch": 36869625,
+            "algorithmic_bytes_per_launch": round(prof["gemm_bytes"] / max(1, prof["gemm_launches"])),
             "flops_per_step": prof["gemm_flops"],
             "launches_per_step": prof["gemm_launches"],
-            "avg_launch_us": round(prof["gemm_ms"] * 1e3 / max(1, prof["gemm_launches"]), 2),
-            "gemm_ms_per_step": round(prof["gemm_ms"], 4),
+            "avg_launch_us": round(gemm_ms * 1e3 / max(1, prof["gemm_launches"]), 2),
+            "gemm_ms_per_step": round(gemm_ms, 4),
+            "timing": "HIP events on the program's stream around 10 back-to-back repeats of "
+                      "each GEMM launch of one eager step",
+            "gemm_ms_in_eager_step": round(prof["gemm_ms"], 4),
             "attention_ms_per_step": round(prof["attention_ms"], 4),
             "eager_step_ms": round(prof["step_ms"], 4),
         },
         "gemm_d1024": d1024,
+        "kernel_configs": kernels,
         "scaled_gpt": None if args.skip_scaled else scaled_gpt(5, 256),
         "loss": round(loss, 4),
     }

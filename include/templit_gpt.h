@@ -98,13 +98,23 @@ int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t pro
 /* Squared gradient norm of the last step (host read, synchronous). */
 int tlg_last_squared_norm(void *program, float *host_value);
 
-/* One eager training step with HIP events recorded on the program's stream
- * around every GEMM launch and every attention launch: returns the summed
- * GEMM time (ms), the GEMMs' algorithmic flops (2*M*N*K each), the number
- * of GEMM launches, the summed attention time and the whole step's time. */
+/* One eager training step, every launch on the program's stream, with HIP
+ * events around every GEMM launch and every attention launch: returns the
+ * summed GEMM time (ms), the GEMMs' algorithmic flops (2*M*N*K each) and
+ * algorithmic HBM bytes (every operand read once, every result written
+ * once: A, B, C, bias, residual, beta*C, the GELU pre-activation, the bias
+ * gradient), the number of GEMM launches, the summed attention time and the
+ * whole step's time. */
 int tlg_profile_step(void *program, float root_grad, float max_norm, float *host_gemm_ms,
-                     double *host_gemm_flops, uint32_t *host_gemm_launches,
-                     float *host_attention_ms, float *host_step_ms);
+                     double *host_gemm_flops, double *host_gemm_bytes,
+                     uint32_t *host_gemm_launches, float *host_attention_ms,
+                     float *host_step_ms);
+
+/* Kernel time of the GEMMs of the last tlg_profile_step: each of its GEMM
+ * launches is repeated `iters` times back to back between two HIP events on
+ * the program's stream; *host_ms = sum over the step's launches of the
+ * per-launch time (ms). Rewrites the step's scratch and gradient buffers. */
+int tlg_time_gemms(void *program, uint32_t iters, float *host_ms);
 
 /* Records tlg_train_step(root_grad, max_norm, 1) as a hipGraph; replays it. */
 int tlg_capture_train_step(void *program, float root_grad, float max_norm);

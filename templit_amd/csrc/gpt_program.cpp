@@ -86,7 +86,8 @@ struct Program {
   std::vector<void *> events;
   size_t next_event = 0;
   std::vector<std::pair<void *, void *>> gemm_spans, attn_spans;
-  double gemm_flops = 0.0;
+  double gemm_flops = 0.0, gemm_bytes = 0.0;
+  std::vector<tlh_gemm_desc> gemm_descs; // the profiled step's GEMMs, in launch order
 
   float *P(uint32_t i) const { return params + offset[i]; }
   float *G(uint32_t i) const { return grads + offset[i]; }
@@ -228,7 +229,17 @@ int gemm(Program &p, tlh_gemm_desc d, bool side = false) {
   const bool on_side = side && concurrent(p);
   // tall-K products may split K; each stream has its own workspace
   if (d.trans_a || d.sum_batches) d.workspace = on_side ? p.workspace_side : p.workspace;
-  if (p.profiling) p.gemm_flops += 2.0 * d.m * double(d.n) * d.k * (d.batch > 1 ? d.batch : 1);
+  if (p.profiling) {
+    const double e = d.batch > 1 ? d.batch : 1, mn = double(d.m) * d.n;
+    const double a = (e > 1 && d.batch_stride_a == 0) ? 1 : e;
+    const double b = (e > 1 && d.batch_stride_b == 0) ? 1 : e;
+    const double c = d.sum_batches ? 1 : e;
+    p.gemm_flops += 2.0 * mn * d.k * e;
+    p.gemm_descs.push_back(d);
+    p.gemm_bytes += 4.0 * (a * d.m * d.k + b * double(d.k) * d.n + c * mn * (d.beta != 0.0f ? 2 : 1) +
+                           (d.residual ? mn : 0) + (d.aux ? mn : 0) + (d.bias ? c * d.n : 0) +
+                           (d.bias_grad ? c * d.n : 0));
+  }
   return timed(p, p.gemm_spans, [&] { return tlh_gemm(&d, on_side ? p.side : p.stream); });
 }
 
@@ -744,7 +755,8 @@ int tlg_last_squared_norm(void *program, float *host_value) {
 }
 
 int tlg_profile_step(void *program, float root_grad, float max_norm, float *host_gemm_ms,
-                     double *host_gemm_flops, uint32_t *host_gemm_launches,
+                     double *host_gemm_flops, double *host_gemm_bytes,
+                     uint32_t *host_gemm_launches,
                      float *host_attention_ms, float *host_step_ms) {
   Program *p = static_cast<Program *>(program);
   TRY(tlh_stream_synchronize(p->stream));
@@ -753,6 +765,8 @@ int tlg_profile_step(void *program, float root_grad, float max_norm, float *host
   p->gemm_spans.clear();
   p->attn_spans.clear();
   p->gemm_flops = 0.0;
+  p->gemm_bytes = 0.0;
+  p->gemm_descs.clear();
   void *start = event(*p), *end = event(*p);
   int st = (start && end) ? tlh_event_record(start, p->stream) : 1;
   if (!st) st = train_step(*p, root_grad, max_norm, 1);
@@ -773,9 +787,36 @@ int tlg_profile_step(void *program, float root_grad, float max_norm, float *host
   TRY(tlh_event_elapsed_ms(start, end, &ms));
   *host_gemm_ms = total;
   *host_gemm_flops = p->gemm_flops;
+  *host_gemm_bytes = p->gemm_bytes;
   *host_gemm_launches = uint32_t(p->gemm_spans.size());
   *host_attention_ms = attn;
   *host_step_ms = ms;
+  return 0;
+}
+
+int tlg_time_gemms(void *program, uint32_t iters, float *host_ms) {
+  Program *p = static_cast<Program *>(program);
+  if (iters == 0 || p->gemm_descs.empty()) return kInvalidValue;
+  TRY(tlh_stream_synchronize(p->stream));
+  void *a = nullptr, *b = nullptr;
+  TRY(tlh_event_create(&a));
+  int st = tlh_event_create(&b);
+  float total = 0.0f;
+  for (size_t i = 0; !st && i < p->gemm_descs.size(); ++i) {
+    const tlh_gemm_desc &d = p->gemm_descs[i];
+    st = tlh_gemm(&d, p->stream); // warm-up
+    if (!st) st = tlh_event_record(a, p->stream);
+    for (uint32_t r = 0; !st && r < iters; ++r) st = tlh_gemm(&d, p->stream);
+    if (!st) st = tlh_event_record(b, p->stream);
+    if (!st) st = tlh_event_synchronize(b);
+    float ms = 0.0f;
+    if (!st) st = tlh_event_elapsed_ms(a, b, &ms);
+    total += ms / float(iters);
+  }
+  tlh_event_destroy(a);
+  if (b) tlh_event_destroy(b);
+  TRY(st);
+  *host_ms = total;
   return 0;
 }
 

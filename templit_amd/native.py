@@ -217,7 +217,9 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_generate_greedy": [P, P, c_uint32, c_uint32, c_uint32, c_int, P],
     "tlg_last_squared_norm": [P, POINTER(c_float)],
     "tlg_profile_step": [P, c_float, c_float, POINTER(c_float), POINTER(ctypes.c_double),
-                         POINTER(c_uint32), POINTER(c_float), POINTER(c_float)],
+                         POINTER(ctypes.c_double), POINTER(c_uint32), POINTER(c_float),
+                         POINTER(c_float)],
+    "tlg_time_gemms": [P, c_uint32, POINTER(c_float)],
     "tlg_capture_train_step": [P, c_float, c_float],
     "tlg_replay": [P],
 }
@@ -381,12 +383,20 @@ class GptProgram:
         check(self.lib.tlg_capture_train_step(self.handle, root_grad, max_norm), "capture")
 
     def profile_step(self, root_grad, max_norm):
-        gm, fl, n, am, sm = c_float(), ctypes.c_double(), c_uint32(), c_float(), c_float()
+        gm, am, sm = c_float(), c_float(), c_float()
+        fl, by, n = ctypes.c_double(), ctypes.c_double(), c_uint32()
         check(self.lib.tlg_profile_step(self.handle, root_grad, max_norm, ctypes.byref(gm),
-                                        ctypes.byref(fl), ctypes.byref(n), ctypes.byref(am),
-                                        ctypes.byref(sm)), "profile_step")
-        return dict(gemm_ms=gm.value, gemm_flops=fl.value, gemm_launches=n.value,
-                    attention_ms=am.value, step_ms=sm.value)
+                                        ctypes.byref(fl), ctypes.byref(by), ctypes.byref(n),
+                                        ctypes.byref(am), ctypes.byref(sm)), "profile_step")
+        return dict(gemm_ms=gm.value, gemm_flops=fl.value, gemm_bytes=by.value,
+                    gemm_launches=n.value, attention_ms=am.value, step_ms=sm.value)
+
+    def time_gemms(self, iters=10):
+        """ms per step of the last profiled step's GEMMs, each re-launched
+        `iters` times back to back (kernel time without the step's gaps)."""
+        ms = c_float()
+        check(self.lib.tlg_time_gemms(self.handle, iters, ctypes.byref(ms)), "time_gemms")
+        return ms.value
 
     def replay(self):
         check(self.lib.tlg_replay(self.handle), "replay")
