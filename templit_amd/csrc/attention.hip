@@ -7,6 +7,13 @@
 // transpose + merge_last_dims -- materialising [B,H,T,T] scores twice.
 // Here each wave keeps 32 query (or key) rows in registers and streams
 // 64-row K/V (or Q/dO) tiles through LDS; scores never reach HBM.
+// A block owns 64 rows (two 32-row tiles) and has 4 waves: wave w works on
+// row tile w%2 and on half w/2 of every streamed 64-row tile, so each
+// 64-row tile feeds four waves and a short sequence still gives every SIMD
+// two or more waves. The two halves' partial results (softmax state and O,
+// or dK/dV, or dQ) are combined through LDS at the end.
+// Grid: x = batch*head, y = 64-row block, ordered so that the blocks with
+// the most causal work are dispatched first (the short ones fill the tail).
 //
 // MFMA v_mfma_f32_32x32x2f32, 64 lanes, r = lane%32, h = lane/32:
 //   A operand: A[m=r][k-slot h];  B operand: B[k-slot h][n=r];
@@ -28,7 +35,7 @@ constexpr int HD = 64;       // head dim
 constexpr int LDP = HD + 4;  // padded LDS row (floats)
 constexpr int KB = 64;       // rows per streamed LDS tile
 constexpr int WQ = 32;       // rows per wave
-constexpr int BQ = 4 * WQ;   // rows per block
+constexpr int BQ = 2 * WQ;   // rows per block (two row tiles x two halves of the stream)
 
 struct Dims {
   uint32_t B, H, T;
@@ -84,21 +91,26 @@ __device__ inline void load_row_half(float (&reg)[32], const float *src, bool va
   }
 }
 
-// Writes each wave's 32x64 result, held transposed in MFMA accumulators
+// Writes a wave's 32x64 result, held transposed in MFMA accumulators
 // (acc[dt][v] = X[row r][dim 32dt + key_of(v,h)]), through LDS so that the
 // global stores are row-contiguous float4s. Called by every wave of the
-// block (it contains barriers); rows >= T are not stored.
+// block (it contains barriers); only waves with `store` write; rows >= T
+// are not stored.
 __device__ inline void store_rows_via_lds(float *smem, const f16x (&acc)[2], float mul,
                                           float *dst_base, const Dims &d, uint32_t b,
-                                          uint32_t h, int row0, int merged, int lane, int wave) {
+                                          uint32_t h, int row0, int merged, int lane, int wave,
+                                          bool store) {
   float *wave_lds = smem + wave * WQ * LDP;
   const int r = lane & 31, hh = lane >> 5;
   __syncthreads();
+  if (store) {
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) wave_lds[r * LDP + 32 * dt + key_of(v, hh)] = acc[dt][v] * mul;
+      for (int v = 0; v < 16; ++v) wave_lds[r * LDP + 32 * dt + key_of(v, hh)] = acc[dt][v] * mul;
+  }
   __syncthreads();
+  if (!store) return;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = i * 4 + (lane >> 4), c4 = lane & 15;
@@ -110,10 +122,32 @@ __device__ inline void store_rows_via_lds(float *smem, const f16x (&acc)[2], flo
   }
 }
 
+// Adds the accumulators of the half-1 wave of each row tile into the half-0
+// wave's (waves rt and rt+2). Called by every wave (barriers); smem must be
+// free and hold NACC * 16 * 64 floats per row tile.
+template <int NACC>
+__device__ inline void sum_halves(float *smem, f16x (&acc)[NACC], int lane, int rt, int half) {
+  float *buf = smem + rt * NACC * 16 * 64;
+  __syncthreads();
+  if (half == 1) {
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) buf[(a * 16 + i) * 64 + lane] = acc[a][i];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][i] += buf[(a * 16 + i) * 64 + lane];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__ q,
+__global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restrict__ q,
                                                        const float *__restrict__ k,
                                                        const float *__restrict__ v,
                                                        float *__restrict__ o,
@@ -124,10 +158,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
   float *Vs = smem + KB * LDP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, hh = lane >> 5;
-  const uint32_t bh = blockIdx.y;
+  const int rt = wave & 1, half = wave >> 1; // row tile; half of each key tile
+  const uint32_t bh = blockIdx.x;
   const uint32_t b = bh / d.H, h = bh % d.H;
-  const int q_block = blockIdx.x * BQ;
-  const int q0 = q_block + wave * WQ;
+  const int q_block = int(gridDim.y - 1 - blockIdx.y) * BQ; // latest queries first
+  const int q0 = q_block + rt * WQ;
   const int my_q = q0 + r;
   const bool active = q0 < int(d.T);
 
@@ -150,56 +185,46 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
   fetch_tile(kpre, k, d, b, h, 0, 0);
   fetch_tile(vpre, v, d, b, h, 0, 0);
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * KB;
+    const int k0 = kb * KB + half * WQ; // this wave's 32 keys of the tile
     __syncthreads(); // every wave is done with the previous tile
     put_tile(Ks, kpre);
     put_tile(Vs, vpre);
     __syncthreads();
     if (kb + 1 < nkb) {
-      fetch_tile(kpre, k, d, b, h, k0 + KB, 0);
-      fetch_tile(vpre, v, d, b, h, k0 + KB, 0);
+      fetch_tile(kpre, k, d, b, h, (kb + 1) * KB, 0);
+      fetch_tile(vpre, v, d, b, h, (kb + 1) * KB, 0);
     }
-    if (!active || (causal && k0 > q0 + WQ - 1)) continue;
-    f16x st[2];
+    if (!active || k0 >= int(d.T) || (causal && k0 > q0 + WQ - 1)) continue;
+    const float *Kh = Ks + half * WQ * LDP, *Vh = Vs + half * WQ * LDP;
+    f16x st;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st[mt][i] = 0.f;
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      f4 ka[2];
+      const f4 ka = *reinterpret_cast<const f4 *>(Kh + r * LDP + 32 * hh + 4 * s4);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-        ka[mt] = *reinterpret_cast<const f4 *>(Ks + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) st[mt] = mfma(ka[mt][j], qreg[4 * s4 + j], st[mt]);
+      for (int j = 0; j < 4; ++j) st = mfma(ka[j], qreg[4 * s4 + j], st);
     }
-    // scale, mask, online softmax (per query = r; keys spread over v, mt, h)
+    // scale, mask, online softmax (per query = r; keys spread over v and h)
     float mx = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = k0 + 32 * mt + key_of(i, hh);
-        float sv = st[mt][i] * scale;
-        if (key >= int(d.T) || (causal && key > my_q)) sv = -INFINITY;
-        st[mt][i] = sv;
-        mx = fmaxf(mx, sv);
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int key = k0 + key_of(i, hh);
+      float sv = st[i] * scale;
+      if (key >= int(d.T) || (causal && key > my_q)) sv = -INFINITY;
+      st[i] = sv;
+      mx = fmaxf(mx, sv);
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     float ps = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = expf(st[mt][i] - m_use);
-        st[mt][i] = p;
-        ps += p;
-      }
+    for (int i = 0; i < 16; ++i) {
+      const float p = expf(st[i] - m_use);
+      st[i] = p;
+      ps += p;
+    }
     ps += __shfl_xor(ps, 32, 64);
     const float alpha = expf(m_run - m_use);
     l_run = l_run * alpha + ps;
@@ -208,21 +233,49 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
-    // O^T += V^T . P^T ; step s -> (mt, i) = (s/16, s%16), key = 32mt + key_of(i, hh)
+    // O^T += V^T . P^T ; step i -> key key_of(i, hh) of this wave's 32
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      const int mt = s >> 4, i = s & 15;
-      const int key = 32 * mt + key_of(i, hh);
+    for (int i = 0; i < 16; ++i) {
+      const int key = key_of(i, hh);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) oacc[dt] = mfma(Vh[key * LDP + 32 * dt + r], st[i], oacc[dt]);
+    }
+  }
+  // combine the two key halves of each query: half 1 hands (m, l, O) to half 0
+  {
+    float *buf = smem + rt * (2 * 16 * 64 + 2 * WQ);
+    __syncthreads(); // every wave is done with Ks/Vs
+    if (half == 1) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
-        oacc[dt] = mfma(Vs[key * LDP + 32 * dt + r], st[mt][i], oacc[dt]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) buf[(dt * 16 + i) * 64 + lane] = oacc[dt][i];
+      if (hh == 0) {
+        buf[2 * 16 * 64 + r] = m_run;
+        buf[2 * 16 * 64 + WQ + r] = l_run;
+      }
+    }
+    __syncthreads();
+    if (half == 0) {
+      const float m1 = buf[2 * 16 * 64 + r], l1 = buf[2 * 16 * 64 + WQ + r];
+      const float m = fmaxf(m_run, m1);
+      const float mu = (m == -INFINITY) ? 0.f : m;
+      const float a0 = expf(m_run - mu), a1 = expf(m1 - mu);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          oacc[dt][i] = oacc[dt][i] * a0 + buf[(dt * 16 + i) * 64 + lane] * a1;
+      l_run = l_run * a0 + l1 * a1;
+      m_run = m;
     }
   }
   // epilogue: O = O / l ; lse = m + log(l)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
-  if (active && hh == 0 && my_q < int(d.T))
+  if (active && half == 0 && hh == 0 && my_q < int(d.T))
     lse[(size_t(b) * d.H + h) * d.T + my_q] = m_run + logf(l_run);
-  store_rows_via_lds(smem, oacc, inv_l, o, d, b, h, q0, o_merged, lane, wave);
+  store_rows_via_lds(smem, oacc, inv_l, o, d, b, h, q0, o_merged, lane, wave,
+                     active && half == 0);
 }
 
 // delta[b,h,t] = sum_d dO[t,d] * O[t,d]
@@ -261,10 +314,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
   float *delta_s = lse_s + KB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, hh = lane >> 5;
-  const uint32_t bh = blockIdx.y;
+  const int rt = wave & 1, half = wave >> 1; // key tile; half of each query tile
+  const uint32_t bh = blockIdx.x;
   const uint32_t b = bh / d.H, h = bh % d.H;
-  const int k_block = blockIdx.x * BQ;
-  const int key0 = k_block + wave * WQ;
+  const int k_block = int(blockIdx.y) * BQ; // earliest keys (most queries) first
+  const int key0 = k_block + rt * WQ;
   const int my_key = key0 + r;
   const bool active = key0 < int(d.T);
 
@@ -274,14 +328,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
   load_row_half(kreg, k + koff, kvalid);
   load_row_half(vreg, v + koff, kvalid);
 
-  f16x dk_acc[2], dv_acc[2];
+  f16x acc[4]; // dk (dt 0, 1), dv (dt 0, 1)
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      dk_acc[dt][i] = 0.f;
-      dv_acc[dt][i] = 0.f;
-    }
+    for (int i = 0; i < 16; ++i) acc[a][i] = 0.f;
 
   const size_t lse_base = (size_t(b) * d.H + h) * d.T;
   const int q_start = causal ? (k_block / KB) * KB : 0;
@@ -310,57 +361,50 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
     }
     __syncthreads();
     if (qt0 + KB < int(d.T)) fetch_q(qt0 + KB);
-    if (!active || (causal && qt0 + KB - 1 < key0)) continue;
-    // S[q][key] for 64 queries (mt) x 32 keys
-    f16x sp[2], dp[2];
+    const int qh0 = qt0 + half * WQ; // this wave's 32 queries of the tile
+    if (!active || qh0 >= int(d.T) || (causal && qh0 + WQ - 1 < key0)) continue;
+    const float *Qh = Qs + half * WQ * LDP, *dOh = dOs + half * WQ * LDP;
+    const float *lse_h = lse_s + half * WQ, *delta_h = delta_s + half * WQ;
+    // S[q][key] for 32 queries x 32 keys
+    f16x sp, dp;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sp[mt][i] = 0.f;
-        dp[mt][i] = 0.f;
-      }
+    for (int i = 0; i < 16; ++i) {
+      sp[i] = 0.f;
+      dp[i] = 0.f;
+    }
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      f4 qa[2], da[2];
+      const f4 qa = *reinterpret_cast<const f4 *>(Qh + r * LDP + 32 * hh + 4 * s4);
+      const f4 da = *reinterpret_cast<const f4 *>(dOh + r * LDP + 32 * hh + 4 * s4);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        qa[mt] = *reinterpret_cast<const f4 *>(Qs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
-        da[mt] = *reinterpret_cast<const f4 *>(dOs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+      for (int j = 0; j < 4; ++j) {
+        sp = mfma(qa[j], kreg[4 * s4 + j], sp);
+        dp = mfma(da[j], vreg[4 * s4 + j], dp);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          sp[mt] = mfma(qa[mt][j], kreg[4 * s4 + j], sp[mt]);
-          dp[mt] = mfma(da[mt][j], vreg[4 * s4 + j], dp[mt]);
-        }
     }
     // P = exp(S*scale - lse[q]) masked; dS = P * (dP - delta[q])
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ql = 32 * mt + key_of(i, hh);
-        const int qq = qt0 + ql;
-        float p = expf(sp[mt][i] * scale - lse_s[ql]);
-        if (qq >= int(d.T) || my_key >= int(d.T) || (causal && my_key > qq)) p = 0.f;
-        sp[mt][i] = p;
-        dp[mt][i] = p * (dp[mt][i] - delta_s[ql]);
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int ql = key_of(i, hh);
+      const int qq = qh0 + ql;
+      float p = expf(sp[i] * scale - lse_h[ql]);
+      if (qq >= int(d.T) || my_key >= int(d.T) || (causal && my_key > qq)) p = 0.f;
+      sp[i] = p;
+      dp[i] = p * (dp[i] - delta_h[ql]);
+    }
     // dV[key][dim] += P^T . dO ; dK[key][dim] += dS^T . Q
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      const int mt = s >> 4, i = s & 15;
-      const int ql = 32 * mt + key_of(i, hh);
+    for (int i = 0; i < 16; ++i) {
+      const int ql = key_of(i, hh);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        dv_acc[dt] = mfma(sp[mt][i], dOs[ql * LDP + 32 * dt + r], dv_acc[dt]);
-        dk_acc[dt] = mfma(dp[mt][i], Qs[ql * LDP + 32 * dt + r], dk_acc[dt]);
+        acc[2 + dt] = mfma(sp[i], dOh[ql * LDP + 32 * dt + r], acc[2 + dt]);
+        acc[dt] = mfma(dp[i], Qh[ql * LDP + 32 * dt + r], acc[dt]);
       }
     }
   }
-  if (!active) return;
+  sum_halves<4>(smem, acc, lane, rt, half);
+  if (!active || half != 0) return;
   // accumulators: D[m = key key_of(v,h)][n = dim r + 32dt] -> row-contiguous stores
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
@@ -369,8 +413,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
       const int key = key0 + key_of(i, hh);
       if (key < int(d.T)) {
         const size_t off = row_off(d, b, h, key, dqkv_merged) + 32 * dt + r;
-        dk[off] = dk_acc[dt][i] * scale;
-        dv[off] = dv_acc[dt][i];
+        dk[off] = acc[dt][i] * scale;
+        dv[off] = acc[2 + dt][i];
       }
     }
 }
@@ -390,10 +434,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
   float *Vs = smem + KB * LDP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, hh = lane >> 5;
-  const uint32_t bh = blockIdx.y;
+  const int rt = wave & 1, half = wave >> 1; // query tile; half of each key tile
+  const uint32_t bh = blockIdx.x;
   const uint32_t b = bh / d.H, h = bh % d.H;
-  const int q_block = blockIdx.x * BQ;
-  const int q0 = q_block + wave * WQ;
+  const int q_block = int(gridDim.y - 1 - blockIdx.y) * BQ; // latest queries first
+  const int q0 = q_block + rt * WQ;
   const int my_q = q0 + r;
   const bool active = q0 < int(d.T);
   const bool qvalid = my_q < int(d.T);
@@ -418,60 +463,52 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
   fetch_tile(kpre, k, d, b, h, 0, 0);
   fetch_tile(vpre, v, d, b, h, 0, 0);
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * KB;
+    const int k0 = kb * KB + half * WQ; // this wave's 32 keys of the tile
     __syncthreads(); // every wave is done with the previous tile
     put_tile(Ks, kpre);
     put_tile(Vs, vpre);
     __syncthreads();
     if (kb + 1 < nkb) {
-      fetch_tile(kpre, k, d, b, h, k0 + KB, 0);
-      fetch_tile(vpre, v, d, b, h, k0 + KB, 0);
+      fetch_tile(kpre, k, d, b, h, (kb + 1) * KB, 0);
+      fetch_tile(vpre, v, d, b, h, (kb + 1) * KB, 0);
     }
-    if (!active || (causal && k0 > q0 + WQ - 1)) continue;
-    f16x st[2], dpt[2];
+    if (!active || k0 >= int(d.T) || (causal && k0 > q0 + WQ - 1)) continue;
+    const float *Kh = Ks + half * WQ * LDP, *Vh = Vs + half * WQ * LDP;
+    f16x st, dpt;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        st[mt][i] = 0.f;
-        dpt[mt][i] = 0.f;
-      }
+    for (int i = 0; i < 16; ++i) {
+      st[i] = 0.f;
+      dpt[i] = 0.f;
+    }
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      f4 ka[2], va[2];
+      const f4 ka = *reinterpret_cast<const f4 *>(Kh + r * LDP + 32 * hh + 4 * s4);
+      const f4 va = *reinterpret_cast<const f4 *>(Vh + r * LDP + 32 * hh + 4 * s4);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        ka[mt] = *reinterpret_cast<const f4 *>(Ks + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
-        va[mt] = *reinterpret_cast<const f4 *>(Vs + (32 * mt + r) * LDP + 32 * hh + 4 * s4);
+      for (int j = 0; j < 4; ++j) {
+        st = mfma(ka[j], qreg[4 * s4 + j], st);
+        dpt = mfma(va[j], doreg[4 * s4 + j], dpt);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          st[mt] = mfma(ka[mt][j], qreg[4 * s4 + j], st[mt]);
-          dpt[mt] = mfma(va[mt][j], doreg[4 * s4 + j], dpt[mt]);
-        }
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = k0 + 32 * mt + key_of(i, hh);
-        float p = expf(st[mt][i] * scale - my_lse);
-        if (!qvalid || key >= int(d.T) || (causal && key > my_q)) p = 0.f;
-        dpt[mt][i] = p * (dpt[mt][i] - my_delta);
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int key = k0 + key_of(i, hh);
+      float p = expf(st[i] * scale - my_lse);
+      if (!qvalid || key >= int(d.T) || (causal && key > my_q)) p = 0.f;
+      dpt[i] = p * (dpt[i] - my_delta);
+    }
     // dQ^T[dim][q] += K^T[dim][key] . dS^T[key][q]
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      const int mt = s >> 4, i = s & 15;
-      const int key = 32 * mt + key_of(i, hh);
+    for (int i = 0; i < 16; ++i) {
+      const int key = key_of(i, hh);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
-        dq_acc[dt] = mfma(Ks[key * LDP + 32 * dt + r], dpt[mt][i], dq_acc[dt]);
+        dq_acc[dt] = mfma(Kh[key * LDP + 32 * dt + r], dpt[i], dq_acc[dt]);
     }
   }
-  store_rows_via_lds(smem, dq_acc, scale, dq, d, b, h, q0, dqkv_merged, lane, wave);
+  sum_halves<2>(smem, dq_acc, lane, rt, half);
+  store_rows_via_lds(smem, dq_acc, scale, dq, d, b, h, q0, dqkv_merged, lane, wave,
+                     active && half == 0);
 }
 
 } // namespace
@@ -482,9 +519,10 @@ TLH_API int tlh_attention_forward(const float *q, const float *k, const float *v
                                   void *stream) {
   if (head_dim != HD) return int(hipErrorInvalidValue);
   if (size_t(batch) * heads * seq == 0) return 0;
-  if (size_t(batch) * heads > 65535) return int(hipErrorInvalidValue);
+  if (ceil_div(seq, BQ) > 65535 || size_t(batch) * heads > 0x7fffffffu)
+    return int(hipErrorInvalidValue);
   const Dims d{batch, heads, seq};
-  dim3 grid(ceil_div(seq, BQ), batch * heads);
+  dim3 grid(batch * heads, ceil_div(seq, BQ));
   attn_fwd_kernel<<<grid, 256, 0, as_stream(stream)>>>(q, k, v, o, lse, d, scale, causal,
                                                        o_merged);
   return launch_status();
@@ -498,14 +536,15 @@ TLH_API int tlh_attention_backward(const float *q, const float *k, const float *
                                    int dqkv_merged, void *stream) {
   if (head_dim != HD) return int(hipErrorInvalidValue);
   if (size_t(batch) * heads * seq == 0) return 0;
-  if (size_t(batch) * heads > 65535) return int(hipErrorInvalidValue);
+  if (ceil_div(seq, BQ) > 65535 || size_t(batch) * heads > 0x7fffffffu)
+    return int(hipErrorInvalidValue);
   hipStream_t s = as_stream(stream);
   const Dims d{batch, heads, seq};
   const size_t rows = size_t(batch) * heads * seq;
   attn_delta_kernel<<<stride_grid(rows * 64, 256), 256, 0, s>>>(o, do_, delta, d, o_merged);
   int st = launch_status();
   if (st) return st;
-  dim3 grid(ceil_div(seq, BQ), batch * heads);
+  dim3 grid(batch * heads, ceil_div(seq, BQ));
   attn_bwd_kv_kernel<<<grid, 256, 0, s>>>(q, k, v, do_, lse, delta, dk, dv, d, scale, causal,
                                           o_merged, dqkv_merged);
   if ((st = launch_status())) return st;

@@ -651,7 +651,9 @@ def test_adamw_multi_matches_per_tensor(g):
 # attention
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("B,H,T,causal", [(4, 6, 192, True), (2, 3, 100, True),
-                                          (2, 2, 130, False), (1, 1, 1, True)])
+                                          (2, 2, 130, False), (1, 1, 1, True),
+                                          (2, 2, 65, True), (3, 1, 33, False),
+                                          (1, 4, 257, True), (1, 2, 1024, True)])
 @pytest.mark.parametrize("merged", [False, True])
 def test_attention_forward_backward(g, B, H, T, causal, merged):
     D = 64
