@@ -207,7 +207,7 @@ typedef struct tlh_gemm_desc {
   const float *bias;     /* [N] or NULL */
   const float *residual; /* indexed like c, or NULL */
   float *aux;            /* GELU pre-activation, indexed like c, or NULL */
-  float *workspace;      /* split-K partials, tlh_gemm_workspace_size elems */
+  float *workspace;      /* partials, tlh_gemm_workspace_size elems (or NULL) */
   int32_t m, n, k;
   int32_t lda, ldb, ldc;
   int32_t trans_a, trans_b;
@@ -232,6 +232,13 @@ typedef struct tlh_gemm_desc {
   int32_t batch;
   uint32_t batch_stride_a, batch_stride_b, batch_stride_c, bias_batch_stride;
   int32_t sum_batches;
+  /* fp32 elements available at `workspace`; 0 = sized with
+   * tlh_gemm_workspace_size for this descriptor. Besides split-K partials
+   * the workspace holds the K-chunk partials of a tail split: when the
+   * output tiles do not spread evenly over the CUs, the tiles beyond a
+   * multiple of the CU count are cut into K chunks and summed in a fixed
+   * order afterwards (used only when the workspace is large enough). */
+  size_t workspace_elems;
 } tlh_gemm_desc;
 
 int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
@@ -243,7 +250,8 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * automatic plan. Process-wide, for measurement sweeps. A forced split
  * count needs a workspace sized for it (tlh_gemm_workspace_size).
  * bk = -1 / -2 instead switches the XCD-aware block order off / on
- * (default on) and leaves the plan alone. */
+ * (default on), bk = -3 / -4 the tail split off / on (default on); both
+ * leave the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

@@ -2,6 +2,7 @@
 // points and the GPT step program).
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
 
 namespace tlh {
@@ -50,6 +51,9 @@ struct GemmDesc {
   // [splits, N] bias-gradient partials) and a reduction kernel applies the
   // epilogue in a fixed order.
   float *workspace = nullptr;
+  // Elements available at `workspace` (0: sized by gemm_workspace_elems for
+  // this descriptor). A tail split that needs more is not used.
+  size_t workspace_elems = 0;
 };
 
 // Launches the GEMM described by `d` on `stream`. Returns hipError_t.

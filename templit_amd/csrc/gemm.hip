@@ -19,6 +19,7 @@
 #include "gemm.h"
 
 #include <algorithm>
+#include <numeric>
 
 namespace tlh {
 namespace {
@@ -53,6 +54,11 @@ struct GemmParams {
   // k / seg_k, whose A and B start seg_a / seg_b elements further on.
   int seg_k;
   uint32_t seg_a, seg_b;
+  // Tail split (batch 1, no split-K): tiles [0, dp_tiles) are whole-K blocks
+  // (a multiple of the CU count); each remaining tile is split into
+  // tail_splits K chunks of tail_k_chunk whose partial tiles go to the
+  // workspace ([tail tile][split][BM*BN]) for gemm_tail_reduce. 0 = off.
+  int dp_tiles, tail_tiles, tail_splits, tail_k_chunk;
 };
 
 __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
@@ -83,6 +89,7 @@ __device__ inline void epilogue_store(const GemmParams &p, const float *bias, fl
 
 // One block's output tile, K range and operand bases.
 struct BlockCtx {
+  bool partial; // a tail-split block: raw partial tile into the workspace
   int tm, m0, n0;
   int k_begin, k_end;
   const float *A, *B;
@@ -98,10 +105,16 @@ __device__ inline BlockCtx block_ctx(const GemmParams &p) {
   // x % 8), each with its own L2. Give XCD j the contiguous tile range
   // [j*G/8, (j+1)*G/8): tiles of the same tile row then share their A rows
   // (and neighbouring rows their B columns) in one L2.
-  const int nblk = int(gridDim.x);
-  const int tile = (p.xcd_remap && (nblk & 7) == 0)
-                       ? int(blockIdx.x & 7) * (nblk >> 3) + int(blockIdx.x >> 3)
-                       : int(blockIdx.x);
+  const int bx = int(blockIdx.x);
+  b.partial = p.tail_splits > 0 && bx >= p.dp_tiles;
+  const int nblk = p.tail_splits > 0 ? p.dp_tiles : int(gridDim.x);
+  int tile = (p.xcd_remap && (nblk & 7) == 0) ? (bx & 7) * (nblk >> 3) + (bx >> 3) : bx;
+  int tail = 0, tail_split = 0;
+  if (b.partial) {
+    tail = (bx - p.dp_tiles) / p.tail_splits;
+    tail_split = bx - p.dp_tiles - tail * p.tail_splits;
+    tile = p.dp_tiles + tail;
+  }
   b.tm = tile / p.tiles_n;
   b.m0 = b.tm * BM;
   b.n0 = (tile - b.tm * p.tiles_n) * BN;
@@ -138,6 +151,11 @@ __device__ inline BlockCtx block_ctx(const GemmParams &p) {
     b.k_end = min(p.K, b.k_begin + p.k_chunk);
     b.C = p.workspace + (size_t(zb) * p.splits + zs) * p.M * p.N;
   }
+  if (b.partial) {
+    b.k_begin = tail_split * p.tail_k_chunk;
+    b.k_end = min(p.K, b.k_begin + p.tail_k_chunk);
+    b.C = p.workspace + (size_t(tail) * p.tail_splits + tail_split) * size_t(BM * BN);
+  }
   return b;
 }
 
@@ -164,10 +182,15 @@ __device__ inline void bias_grad_store(const GemmParams &p, const BlockCtx &b, f
   }
 }
 
-// Writes the accumulators of one wave (TM x TN 32x32 tiles) through the epilogue.
-template <int TM, int TN, int WM, int WN, bool FULL>
+// Writes the accumulators of one wave (TM x TN 32x32 tiles) through the
+// epilogue, or raw: into the split-K plane, or into the block's partial
+// tile of a tail split (row-major BM x BN).
+template <int BN, int TM, int TN, int WM, int WN, bool FULL>
 __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f16x (&acc)[TM][TN],
                                  int wm, int wn, int r, int hk) {
+  const bool raw = b.partial || p.splits > 1;
+  const int rs = b.partial ? BN : p.N;
+  float *rbase = b.partial ? b.C - (size_t(b.m0) * BN + b.n0) : b.C;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -178,8 +201,8 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
       for (int v = 0; v < 16; ++v) {
         const int m = b.m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
         if (!FULL && m >= p.M) continue;
-        if (p.splits > 1) {
-          b.C[size_t(m) * p.N + n] = acc[i][j][v];
+        if (raw) {
+          rbase[size_t(m) * rs + n] = acc[i][j][v];
         } else {
           epilogue_store(p, b.bias, b.C, m, n, acc[i][j][v]);
         }
@@ -394,7 +417,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     }
   }
   if (do_bias) bias_grad_store<BN>(p, ctx, smem, bsum, FULL);
-  store_acc<TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
+  store_acc<BN, TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
 }
 
 // Sums the split-K partials of every output entry in split order --
@@ -454,6 +477,29 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
   }
 }
 
+// Sums the tail tiles' K-chunk partials in chunk order -- deterministic --
+// and applies the epilogue. Float4 groups of a BM x BN tile (BN % 4 == 0).
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_tail_reduce(GemmParams p) {
+  constexpr int TILE = BM * BN;
+  const int tails = p.tail_tiles;
+  const size_t groups = size_t(tails) * (TILE / 4);
+  const size_t step = size_t(gridDim.x) * blockDim.x;
+  for (size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x; g < groups; g += step) {
+    const int t = int(g / (TILE / 4));
+    const int e = int(g - size_t(t) * (TILE / 4)) * 4;
+    const f4 *w = reinterpret_cast<const f4 *>(p.workspace + size_t(t) * p.tail_splits * TILE + e);
+    f4 sum = w[0];
+    for (int s = 1; s < p.tail_splits; ++s) sum += w[size_t(s) * (TILE / 4)];
+    const int tile = p.dp_tiles + t;
+    const int tm = tile / p.tiles_n;
+    const int m = tm * BM + e / BN;
+    const int n = (tile - tm * p.tiles_n) * BN + e % BN;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) epilogue_store(p, p.bias, p.C, m, n + q, sum[q]);
+  }
+}
+
 struct Plan {
   int bm, bn, splits, bk = 16;
 };
@@ -491,6 +537,7 @@ constexpr int kTargetBlocks = 256; // one block per CU at least
 // planner decides.
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
 int g_xcd_remap = 1;
+int g_tail_split = 1;
 constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 
 // Tile plan, from measurements on MI355X of the GPT step's shapes
@@ -539,12 +586,65 @@ bool vec_ok(const GemmDesc &d) {
 
 int gemm_choose_splits(const GemmDesc &d) { return make_plan(d, true).splits; }
 
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Tail split of a tile-aligned single product (no split-K, no bias
+// gradient). Its blocks run co-resident, so a CU holding ceil(tiles/CUs)
+// blocks sets the time: 576 tiles on 256 CUs leave 64 CUs with a third
+// block (75% balance). The first floor(tiles/CUs)*CUs tiles stay whole-K
+// blocks; each remaining tile is cut into `splits` K chunks (multiples of
+// kBK, so no K tile straddles a chunk or a K segment) that spread over the
+// CUs, and gemm_tail_reduce sums them.
+constexpr int kMinTailSplitK = 1024;
+
+struct TailSplit {
+  int dp_tiles = 0, tails = 0, splits = 0, k_chunk = 0;
+  size_t elems(const Plan &plan) const { return size_t(tails) * splits * plan.bm * plan.bn; }
+};
+
+TailSplit tail_split(const GemmDesc &d, const Plan &plan, int K) {
+  TailSplit t;
+  if (!g_tail_split || plan.splits > 1 || d.bias_grad || (d.batch > 1 && !d.sum_batches))
+    return t;
+  // the reduction launch costs a few microseconds: only long K ranges gain
+  if (d.M % plan.bm || d.N % plan.bn || K % plan.bk || K < kMinTailSplitK) return t;
+  const int tiles = (d.M / plan.bm) * (d.N / plan.bn);
+  const int cus = cu_count();
+  const int per = tiles / cus, tail = tiles - per * cus;
+  if (per < 1 || tail == 0 || double(tiles) / cus / (per + 1) >= 0.9) return t;
+  int splits = std::min(16, cus / std::gcd(tail, cus));
+  const int chunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+  splits = (K + chunk - 1) / chunk;
+  if (splits < 2) return t;
+  t.dp_tiles = per * cus;
+  t.tails = tail;
+  t.splits = splits;
+  t.k_chunk = chunk;
+  return t;
+}
+
+int folded_k(const GemmDesc &d) { return d.sum_batches ? d.K * d.batch : d.K; }
+
 size_t gemm_workspace_elems(const GemmDesc &d) {
-  const int s = gemm_choose_splits(d);
+  const Plan plan = make_plan(d, true);
+  const int s = plan.splits;
   const size_t outputs = d.sum_batches ? 1 : size_t(std::max(1, d.batch));
   // C partials [outputs, s, M, N] followed by bias-gradient partials
   // [outputs, s, N]
-  return s > 1 ? outputs * size_t(s) * (size_t(d.M) * d.N + d.N) : 0;
+  if (s > 1) return outputs * size_t(s) * (size_t(d.M) * d.N + d.N);
+  return tail_split(d, plan, folded_k(d)).elems(plan); // [tails, splits, bm*bn]
 }
 
 int gemm_launch(const GemmDesc &d, void *stream) {
@@ -585,7 +685,9 @@ int gemm_launch(const GemmDesc &d, void *stream) {
     p.bsb[i] = d.batch_stride_b[i];
     p.bsc[i] = d.batch_stride_c[i];
   }
-  const Plan plan = make_plan(d, d.workspace != nullptr);
+  Plan plan = make_plan(d, d.workspace != nullptr);
+  if (plan.splits > 1 && d.workspace_elems && gemm_workspace_elems(d) > d.workspace_elems)
+    plan = make_plan(d, false); // the given workspace is too small to split K
   p.tiles_n = (d.N + plan.bn - 1) / plan.bn;
   p.xcd_remap = g_xcd_remap;
   const int tiles_m = (d.M + plan.bm - 1) / plan.bm;
@@ -593,14 +695,25 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.k_chunk = p.splits > 1 ? ((K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : K;
   if (p.splits > 1) p.splits = (K + p.k_chunk - 1) / p.k_chunk; // <= plan.splits
   const size_t reduce_elems = size_t(d.M) * d.N;
+  const bool vec = vec_ok(d);
+  TailSplit ts;
+  if (p.splits <= 1 && d.workspace && vec) {
+    ts = tail_split(d, plan, K);
+    if (ts.splits && d.workspace_elems && d.workspace_elems < ts.elems(plan)) ts = TailSplit{};
+  }
+  p.dp_tiles = ts.dp_tiles;
+  p.tail_tiles = ts.tails;
+  p.tail_splits = ts.splits;
+  p.tail_k_chunk = ts.k_chunk;
   if (K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
     gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
     return launch_status();
   }
   const int z = p.splits > 1 ? p.batch * p.splits : p.batch;
-  dim3 grid(unsigned(tiles_m * p.tiles_n), 1, unsigned(z));
-  const bool ta = d.trans_a != 0, tb = d.trans_b != 0, vec = vec_ok(d);
+  const int blocks = ts.splits ? ts.dp_tiles + ts.tails * ts.splits : tiles_m * p.tiles_n;
+  dim3 grid(unsigned(blocks), 1, unsigned(z));
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
   // Every block's K range is a multiple of the K tile when K is and the
   // split chunk (a multiple of kBK) is.
   const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && K % plan.bk == 0 &&
@@ -618,6 +731,15 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   }
   int st = launch_status();
   if (st) return st;
+  if (ts.splits) {
+    const size_t groups = size_t(ts.tails) * plan.bm * plan.bn / 4;
+    const unsigned g = stride_grid(groups, 256);
+    if (plan.bm == 128 && plan.bn == 128) gemm_tail_reduce<128, 128><<<g, 256, 0, s>>>(p);
+    else if (plan.bm == 128) gemm_tail_reduce<128, 64><<<g, 256, 0, s>>>(p);
+    else if (plan.bn == 128) gemm_tail_reduce<64, 128><<<g, 256, 0, s>>>(p);
+    else gemm_tail_reduce<64, 64><<<g, 256, 0, s>>>(p);
+    return launch_status();
+  }
   if (p.splits > 1) {
     // The workspace planes start 16-byte aligned when M*N is a multiple of 4.
     const bool v4 = d.N % 4 == 0 && (reinterpret_cast<uintptr_t>(d.workspace) & 15) == 0;
@@ -643,6 +765,7 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
   d.A = c.a; d.B = c.b; d.C = c.c;
   d.bias = c.bias; d.residual = c.residual; d.aux = c.aux;
   d.workspace = c.workspace;
+  d.workspace_elems = c.workspace_elems;
   d.M = c.m; d.N = c.n; d.K = c.k;
   d.lda = c.lda; d.ldb = c.ldb; d.ldc = c.ldc;
   d.trans_a = c.trans_a; d.trans_b = c.trans_b;
@@ -665,9 +788,14 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
 } // namespace
 
 TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
-  // bk < 0 toggles the XCD-aware block order off (-1) or on (-2) instead.
+  // bk < 0 toggles instead: the XCD-aware block order off (-1) or on (-2),
+  // the tail split off (-3) or on (-4).
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
+    return 0;
+  }
+  if (bk == -3 || bk == -4) {
+    tlh::g_tail_split = bk == -4;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));

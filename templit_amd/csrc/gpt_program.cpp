@@ -227,8 +227,9 @@ int record_side(Program &p, void *ev) {
 
 int gemm(Program &p, tlh_gemm_desc d, bool side = false) {
   const bool on_side = side && concurrent(p);
-  // tall-K products may split K; each stream has its own workspace
-  if (d.trans_a || d.sum_batches) d.workspace = on_side ? p.workspace_side : p.workspace;
+  // partials of split-K and tail-split products; each stream has its own
+  d.workspace = on_side ? p.workspace_side : p.workspace;
+  d.workspace_elems = p.workspace_elems;
   if (p.profiling) {
     const double e = d.batch > 1 ? d.batch : 1, mn = double(d.m) * d.n;
     const double a = (e > 1 && d.batch_stride_a == 0) ? 1 : e;
@@ -496,7 +497,8 @@ int create(Program &p) {
   p.dk = p.dq + R * D;
   p.dv = p.dq + 2 * R * D;
   TRY(allocf(p, &p.delta, B * H * T));
-  // split-K workspace: the largest any weight-gradient GEMM asks for
+  // workspace: the largest any GEMM of the step asks for (split-K weight
+  // gradients; tail splits of the others)
   size_t ws = 0;
   const int shapes[4][2] = {{int(D), int(V)}, {int(F), int(D)}, {int(D), int(F)},
                             {int(D), int(D)}};
@@ -510,6 +512,13 @@ int create(Program &p) {
     qkv_batch(d, uint32_t(R * D), ptrdiff_t(D * D + D));
     d.sum_batches = 1;
     uses.push_back(d);
+  }
+  // linears (out, in): forward x.W and input gradient dY.W^T
+  const int linears[4][2] = {{int(D), int(D)}, {int(F), int(D)}, {int(D), int(F)},
+                             {int(V), int(D)}};
+  for (auto &s : linears) {
+    uses.push_back(desc(nullptr, nullptr, nullptr, int(R), s[0], s[1], false, false));
+    uses.push_back(desc(nullptr, nullptr, nullptr, int(R), s[1], s[0], false, true));
   }
   for (auto &d : uses) {
     size_t e = 0;

@@ -89,8 +89,9 @@ def run_gemm(b: Bench, iters: int, sweep: bool, only: str | None = None) -> None
         d.m, d.n, d.k = M, N, K
         d.lda, d.ldb, d.ldc = (M if ta else K), (K if tb else N), N
         d.trans_a, d.trans_b = ta, tb
+        d.workspace, d.workspace_elems = ws, ws_elems
         if bgrad:
-            d.bias_grad, d.workspace = bias_grad, ws
+            d.bias_grad = bias_grad
         results = []
         for plan in plans:
             if plan[2] > 1 and not bgrad:
@@ -145,10 +146,14 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--only", help="GEMM shapes whose name contains this text")
+    ap.add_argument("--no-tail-split", action="store_true",
+                    help="no K-chunked tail tiles for grids that do not spread evenly")
     args = ap.parse_args()
     if not (args.gemm or args.attention):
         args.gemm = args.attention = True
     b = Bench()
+    if args.no_tail_split:
+        check(b.hip.tlh_gemm_set_plan(0, 0, 0, -3), "plan")
     try:
         if args.gemm:
             run_gemm(b, args.iters, args.sweep, args.only)

@@ -38,6 +38,7 @@ class GemmDesc(ctypes.Structure):
         ("batch_stride_a", c_uint32), ("batch_stride_b", c_uint32),
         ("batch_stride_c", c_uint32), ("bias_batch_stride", c_uint32),
         ("sum_batches", c_int32),
+        ("workspace_elems", c_size_t),
     ]
 
 

@@ -227,6 +227,7 @@ def forced_plan(g):
     """tlh_gemm_set_plan is process-wide: restore the planner afterwards."""
     yield lambda *plan: check(g.lib.tlh_gemm_set_plan(*plan), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, 16), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -4), "set_plan")
 
 
 @pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
@@ -250,6 +251,40 @@ def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
         dw, db = gemm(g, x, dy, ta=True, bias_grad_init=np.zeros(N, np.float32))
         assert_rel(dw.reshape(M, N), O.matmul(x.T, dy), 1e-3, f"dW splits={splits}")
         assert_close(db, O.sum_to_shape(dy, [N]), rtol=1e-4, atol=1e-3, what="db")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("K", [384, 1536])
+def test_gemm_tail_split(g, forced_plan, ta, tb, K):
+    # 6144 x 384 is 576 tiles of 64x64: 512 whole-K blocks (2 per CU) and
+    # 64 tiles cut into K chunks summed afterwards. Same result with the
+    # tail split off, bit-identical run to run, every epilogue input.
+    M, N = 6144, 384
+    a = O.normal((K, M) if ta else (M, K), 160, 0, 0.5)
+    b = O.normal((N, K) if tb else (K, N), 161, 0, 0.5)
+    bias, res, c0 = O.normal((N,), 162), O.normal((M, N), 163), O.normal((M, N), 164)
+    expect = O.matmul(a.T if ta else a, b.T if tb else b) + bias + c0 + res
+    outs = []
+    for on in (True, True, False):
+        forced_plan(0, 0, 0, -4 if on else -3)
+        out, _ = gemm(g, a, b, ta, tb, bias=bias, residual=res, beta=1.0, c_init=c0)
+        assert_rel(out.reshape(M, N), expect, 1e-3, f"tail split {on}")
+        outs.append(out)
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_gemm_tail_split_gelu_epilogues(g):
+    # the tail tiles' reduction applies the GELU forward (writing the
+    # pre-activation) and the GELU' epilogue like the whole-K blocks do
+    M, N, K = 6144, 384, 1536
+    a, b = O.normal((M, K), 165, 0, 0.05), O.normal((K, N), 166, 0, 0.05)
+    bias = O.normal((N,), 167)
+    pre = O.matmul(a, b) + bias
+    out, aux = gemm(g, a, b, bias=bias, epi=EPI_GELU)
+    assert_rel(aux.reshape(M, N), pre, 1e-3, "pre-activation")
+    assert_rel(out.reshape(M, N), O.unary("gelu", pre), 1e-3, "gelu")
+    out, _ = gemm(g, a, b, epi=EPI_GELU_BWD, aux=pre)
+    assert_rel(out.reshape(M, N), O.matmul(a, b) * O.unary("gelu_derivative", pre), 1e-3, "gelu'")
 
 
 def test_gemm_bias_residual_beta(g):
