@@ -285,7 +285,7 @@ int tlh_accumulate_gradient_squared_norm(const float *g, size_t n,
  * include/passes/compile.h:241-245, in one launch): *squared_norm = sum over
  * `count` tensors of g^2. grads / sizes are device arrays; `partials` is
  * device scratch of TLH_NORM_PARTIALS floats. Deterministic (fixed
- * reduction order, no atomics). */
+ * reduction order, no atomics). count <= 2048. */
 #define TLH_NORM_PARTIALS 1024
 int tlh_gradient_squared_norm_multi(const float *const *grads,
                                     const uint64_t *sizes, uint32_t count,
@@ -409,7 +409,7 @@ int tlh_adamw(const float *param, const float *grad, float *out, float *m1,
  * place. Device arrays: params/grads/m1/m2 pointers, sizes, steps (uint32
  * per tensor: the per-parameter step_ of AdamW.h:42,78). If squared_norm
  * != NULL the gradient is scaled by min(1, max_norm/sqrt(max(s,1e-12)))
- * first (Compiled::step(max_norm), compile.h:236-258). */
+ * first (Compiled::step(max_norm), compile.h:236-258). count <= 2048. */
 int tlh_adamw_multi(float *const *params, const float *const *grads,
                     float *const *m1, float *const *m2, const uint64_t *sizes,
                     const uint32_t *steps, uint32_t count, const float *beta1,

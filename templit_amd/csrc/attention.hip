@@ -278,24 +278,6 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
                      active && half == 0);
 }
 
-// delta[b,h,t] = sum_d dO[t,d] * O[t,d]
-__global__ __launch_bounds__(256) void attn_delta_kernel(const float *__restrict__ o,
-                                                         const float *__restrict__ dout,
-                                                         float *__restrict__ delta, Dims d,
-                                                         int merged) {
-  const int lane = threadIdx.x & 63;
-  const size_t rows = size_t(d.B) * d.H * d.T;
-  for (size_t row = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6; row < rows;
-       row += (size_t(gridDim.x) * blockDim.x) >> 6) {
-    const uint32_t t = uint32_t(row % d.T);
-    const uint32_t bh = uint32_t(row / d.T);
-    const size_t off = row_off(d, bh / d.H, bh % d.H, t, merged);
-    float x = o[off + lane] * dout[off + lane];
-    x = wave_sum(x);
-    if (lane == 0) delta[row] = x;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // backward, part 1: dK, dV. Each wave owns 32 keys; query tiles stream
 // through LDS. S = Q.K^T is computed with m = query, n = key, so a lane holds
@@ -426,8 +408,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    const float *__restrict__ dout, const float *__restrict__ lse,
-    const float *__restrict__ delta, float *__restrict__ dq, Dims d, float scale, int causal,
+    const float *__restrict__ o, const float *__restrict__ dout, const float *__restrict__ lse,
+    float *__restrict__ delta, float *__restrict__ dq, Dims d, float scale, int causal,
     int o_merged, int dqkv_merged) {
   __shared__ __attribute__((aligned(16))) float smem[2 * KB * LDP];
   float *Ks = smem;
@@ -445,10 +427,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
 
   float qreg[32], doreg[32];
   load_row_half(qreg, q + row_off(d, b, h, qvalid ? my_q : 0, 0) + 32 * hh, qvalid);
-  load_row_half(doreg, dout + row_off(d, b, h, qvalid ? my_q : 0, o_merged) + 32 * hh, qvalid);
+  const size_t do_off = row_off(d, b, h, qvalid ? my_q : 0, o_merged) + 32 * hh;
+  load_row_half(doreg, dout + do_off, qvalid);
   const size_t lse_base = (size_t(b) * d.H + h) * d.T;
   const float my_lse = qvalid ? lse[lse_base + my_q] : 0.f;
-  const float my_delta = qvalid ? delta[lse_base + my_q] : 0.f;
+  // delta = dO . O for this query (the two lane halves hold 32 dims each);
+  // stored for the dK/dV kernel, which runs next
+  float my_delta = 0.f;
+  {
+    float oreg[32];
+    load_row_half(oreg, o + do_off, qvalid);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) my_delta += oreg[i] * doreg[i];
+    my_delta += __shfl_xor(my_delta, 32, 64);
+    if (qvalid && half == 0 && hh == 0) delta[lse_base + my_q] = my_delta;
+  }
 
   f16x dq_acc[2];
 #pragma unroll
@@ -540,15 +533,13 @@ TLH_API int tlh_attention_backward(const float *q, const float *k, const float *
     return int(hipErrorInvalidValue);
   hipStream_t s = as_stream(stream);
   const Dims d{batch, heads, seq};
-  const size_t rows = size_t(batch) * heads * seq;
-  attn_delta_kernel<<<stride_grid(rows * 64, 256), 256, 0, s>>>(o, do_, delta, d, o_merged);
+  // dQ first: it also computes delta = rowsum(dO * O), which dK/dV need
+  dim3 grid(batch * heads, ceil_div(seq, BQ));
+  attn_bwd_q_kernel<<<grid, 256, 0, s>>>(q, k, v, o, do_, lse, delta, dq, d, scale, causal,
+                                         o_merged, dqkv_merged);
   int st = launch_status();
   if (st) return st;
-  dim3 grid(batch * heads, ceil_div(seq, BQ));
   attn_bwd_kv_kernel<<<grid, 256, 0, s>>>(q, k, v, do_, lse, delta, dk, dv, d, scale, causal,
                                           o_merged, dqkv_merged);
-  if ((st = launch_status())) return st;
-  attn_bwd_q_kernel<<<grid, 256, 0, s>>>(q, k, v, do_, lse, delta, dq, d, scale, causal,
-                                         o_merged, dqkv_merged);
   return launch_status();
 }

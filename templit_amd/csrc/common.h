@@ -96,4 +96,54 @@ __device__ inline float gelu_grad(float x) {
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * kGeluA * (1.0f + 3.0f * kGeluB * x2);
 }
 
+// ---- multi-tensor chunk maps -----------------------------------------------
+// The tensors of a multi-tensor launch are cut into chunks numbered across
+// all tensors; first[t] is tensor t's first chunk and first[count] the total.
+// A block builds the map in LDS (256 threads, count <= kMaxMultiTensors) from
+// chunks_of(t), so that chunk c's tensor is a binary search away instead of
+// a walk over the device-side tensor table.
+constexpr uint32_t kMaxMultiTensors = 2048;
+
+template <typename ChunksOf>
+__device__ inline uint32_t build_chunk_map(uint32_t *first, uint32_t count, ChunksOf chunks_of) {
+  __shared__ uint32_t wave_total[4];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t per = (count + 255) / 256;
+  const uint32_t b = min(count, tid * per), e = min(count, b + per);
+  uint32_t sum = 0;
+  for (uint32_t t = b; t < e; ++t) sum += chunks_of(t);
+  uint32_t incl = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t x = __shfl_up(incl, o, 64);
+    if (int(lane) >= o) incl += x;
+  }
+  if (lane == 63) wave_total[wave] = incl;
+  __syncthreads();
+  uint32_t acc = incl - sum, total = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < 4; ++w) {
+    if (w < wave) acc += wave_total[w];
+    total += wave_total[w];
+  }
+  for (uint32_t t = b; t < e; ++t) { // (chunks_of again: a few table reads)
+    first[t] = acc;
+    acc += chunks_of(t);
+  }
+  if (tid == 0) first[count] = total;
+  __syncthreads();
+  return total;
+}
+
+// The tensor holding chunk c: the last t with first[t] <= c (skips empty tensors).
+__device__ inline uint32_t chunk_owner(const uint32_t *first, uint32_t count, uint32_t c) {
+  uint32_t lo = 0, hi = count; // first[lo] <= c < first[hi]
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (first[mid] <= c) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
 } // namespace tlh

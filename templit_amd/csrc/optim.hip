@@ -61,7 +61,8 @@ __global__ __launch_bounds__(256) void adamw_kernel(const float *param, const fl
 constexpr uint32_t kChunk = 4096; // elements per work item (multiple of 4)
 
 // Multi-tensor clip + AdamW. Work items are (tensor, 4096-element chunk)
-// pairs numbered across all tensors; block b takes items b, b+G, ... .
+// pairs numbered across all tensors (a chunk map in LDS); block b takes
+// items b, b+G, ... .
 __global__ __launch_bounds__(256) void adamw_multi_kernel(
     float *const *__restrict__ params, const float *const *__restrict__ grads,
     float *const *__restrict__ m1s, float *const *__restrict__ m2s,
@@ -69,55 +70,51 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(
     const float *__restrict__ beta1, const float *__restrict__ beta2,
     const float *__restrict__ decay, const float *__restrict__ lr, float eps,
     const float *__restrict__ squared_norm, float max_norm) {
+  __shared__ uint32_t first[kMaxMultiTensors + 1];
+  const uint32_t total = build_chunk_map(
+      first, count, [&](uint32_t t) { return uint32_t((sizes[t] + kChunk - 1) / kChunk); });
   const float b1 = *beta1, b2 = *beta2, dc = *decay, l = *lr;
   const float scale = squared_norm ? clip_scale(*squared_norm, max_norm) : 1.0f;
-  uint64_t item_base = 0;
-  for (uint32_t t = 0; t < count; ++t) {
+  for (uint32_t it = blockIdx.x; it < total; it += gridDim.x) {
+    const uint32_t t = chunk_owner(first, count, it);
     const uint64_t n = sizes[t];
-    const uint64_t items = (n + kChunk - 1) / kChunk;
-    const uint64_t first = (blockIdx.x + gridDim.x - item_base % gridDim.x) % gridDim.x;
-    if (first < items) {
-      float *p = params[t];
-      const float *g = grads[t];
-      float *m1 = m1s[t];
-      float *m2 = m2s[t];
-      const float step = float(steps[t]);
-      const float c1 = 1.0f - powf(b1, step);
-      const float c2 = 1.0f - powf(b2, step);
-      const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
-                         reinterpret_cast<uintptr_t>(m1) | reinterpret_cast<uintptr_t>(m2)) &
-                        15) == 0;
-      for (uint64_t it = first; it < items; it += gridDim.x) {
-        const uint64_t begin = it * kChunk;
-        const uint64_t end = begin + kChunk < n ? begin + kChunk : n;
-        if (vec && end - begin == kChunk) {
-          for (uint64_t i = begin + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
-            f4 pv = *reinterpret_cast<const f4 *>(p + i);
-            const f4 gv = *reinterpret_cast<const f4 *>(g + i);
-            f4 mv = *reinterpret_cast<const f4 *>(m1 + i);
-            f4 vv = *reinterpret_cast<const f4 *>(m2 + i);
+    float *p = params[t];
+    const float *g = grads[t];
+    float *m1 = m1s[t];
+    float *m2 = m2s[t];
+    const float step = float(steps[t]);
+    const float c1 = 1.0f - powf(b1, step);
+    const float c2 = 1.0f - powf(b2, step);
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
+                       reinterpret_cast<uintptr_t>(m1) | reinterpret_cast<uintptr_t>(m2)) &
+                      15) == 0;
+    const uint64_t begin = uint64_t(it - first[t]) * kChunk;
+    const uint64_t end = begin + kChunk < n ? begin + kChunk : n;
+    if (vec && end - begin == kChunk) {
+      for (uint64_t i = begin + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
+        f4 pv = *reinterpret_cast<const f4 *>(p + i);
+        const f4 gv = *reinterpret_cast<const f4 *>(g + i);
+        f4 mv = *reinterpret_cast<const f4 *>(m1 + i);
+        f4 vv = *reinterpret_cast<const f4 *>(m2 + i);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float m = mv[q], vq = vv[q];
-              pv[q] = adamw_update(pv[q], gv[q] * scale, m, vq, b1, b2, dc, l, eps, c1, c2);
-              mv[q] = m;
-              vv[q] = vq;
-            }
-            *reinterpret_cast<f4 *>(p + i) = pv;
-            *reinterpret_cast<f4 *>(m1 + i) = mv;
-            *reinterpret_cast<f4 *>(m2 + i) = vv;
-          }
-        } else {
-          for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
-            float m = m1[i], v = m2[i];
-            p[i] = adamw_update(p[i], g[i] * scale, m, v, b1, b2, dc, l, eps, c1, c2);
-            m1[i] = m;
-            m2[i] = v;
-          }
+        for (int q = 0; q < 4; ++q) {
+          float m = mv[q], vq = vv[q];
+          pv[q] = adamw_update(pv[q], gv[q] * scale, m, vq, b1, b2, dc, l, eps, c1, c2);
+          mv[q] = m;
+          vv[q] = vq;
         }
+        *reinterpret_cast<f4 *>(p + i) = pv;
+        *reinterpret_cast<f4 *>(m1 + i) = mv;
+        *reinterpret_cast<f4 *>(m2 + i) = vv;
+      }
+    } else {
+      for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        float m = m1[i], v = m2[i];
+        p[i] = adamw_update(p[i], g[i] * scale, m, v, b1, b2, dc, l, eps, c1, c2);
+        m1[i] = m;
+        m2[i] = v;
       }
     }
-    item_base += items;
   }
 }
 
@@ -147,6 +144,7 @@ TLH_API int tlh_adamw_multi(float *const *params, const float *const *grads, flo
                             const float *decay, const float *lr, float eps,
                             const float *squared_norm, float max_norm, void *stream) {
   if (count == 0) return 0;
+  if (count > kMaxMultiTensors) return int(hipErrorInvalidValue);
   adamw_multi_kernel<<<1024, 256, 0, as_stream(stream)>>>(params, grads, m1, m2, sizes, steps,
                                                           count, beta1, beta2, decay, lr, eps,
                                                           squared_norm, max_norm);

@@ -287,30 +287,58 @@ constexpr uint32_t kNormChunk = 4096;
 
 // Multi-tensor: every block walks all tensors, taking chunk c of tensor t
 // when c % gridDim.x == blockIdx.x; writes one partial per block.
-__global__ __launch_bounds__(256) void sqnorm_multi_kernel(const float *const *__restrict__ grads,
+__global__ __launch_bounds__(256) void sqnorm_multi_kernel(const float *__restrict__ const *grads,
                                                            const uint64_t *__restrict__ sizes,
                                                            uint32_t count,
                                                            float *__restrict__ partials) {
   __shared__ float scratch[4];
-  float v = 0.0f;
-  uint64_t chunk_base = 0; // global chunk counter across tensors
-  for (uint32_t t = 0; t < count; ++t) {
-    const float *g = grads[t];
+  __shared__ uint32_t first[kMaxMultiTensors + 1];
+  // 16-byte aligned tensors: chunks of 1024 float4 (4096 floats), then the
+  // last n % 4 elements as one more chunk; otherwise scalar chunks of 4096.
+  auto split = [&](uint32_t t, uint64_t &n4, uint32_t &vchunks) {
     const uint64_t n = sizes[t];
-    const uint64_t chunks = (n + kNormChunk - 1) / kNormChunk;
-    // first chunk of this tensor owned by this block
-    uint64_t c0 = (blockIdx.x + gridDim.x - chunk_base % gridDim.x) % gridDim.x;
-    for (uint64_t c = c0; c < chunks; c += gridDim.x) {
-      const uint64_t begin = c * kNormChunk;
+    n4 = (reinterpret_cast<uintptr_t>(grads[t]) & 15) == 0 ? n / 4 : 0;
+    vchunks = uint32_t((n4 + kNormChunk / 4 - 1) / (kNormChunk / 4));
+    return n;
+  };
+  const uint32_t total = build_chunk_map(first, count, [&](uint32_t t) {
+    uint64_t n4;
+    uint32_t vchunks;
+    const uint64_t n = split(t, n4, vchunks);
+    return vchunks + uint32_t((n - 4 * n4 + kNormChunk - 1) / kNormChunk);
+  });
+  float v0 = 0.0f, v1 = 0.0f;
+  for (uint32_t c = blockIdx.x; c < total; c += gridDim.x) {
+    const uint32_t t = chunk_owner(first, count, c);
+    const float *g = grads[t];
+    uint64_t n4;
+    uint32_t vchunks;
+    const uint64_t n = split(t, n4, vchunks);
+    const uint32_t k = c - first[t];
+    if (k < vchunks) {
+      const f4 *g4 = reinterpret_cast<const f4 *>(g);
+      const uint64_t begin = uint64_t(k) * (kNormChunk / 4);
+      const uint64_t end = begin + kNormChunk / 4 < n4 ? begin + kNormChunk / 4 : n4;
+      uint64_t i = begin + threadIdx.x;
+      for (; i + 256 < end; i += 512) { // two loads in flight per thread
+        const f4 x = g4[i], y = g4[i + 256];
+        v0 += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        v1 += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+      }
+      if (i < end) {
+        const f4 x = g4[i];
+        v0 += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+      }
+    } else {
+      const uint64_t begin = 4 * n4 + uint64_t(k - vchunks) * kNormChunk;
       const uint64_t end = begin + kNormChunk < n ? begin + kNormChunk : n;
       for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
         const float x = g[i];
-        v += x * x;
+        v0 += x * x;
       }
     }
-    chunk_base += chunks;
   }
-  v = block_sum(v, scratch);
+  const float v = block_sum(v0 + v1, scratch);
   if (threadIdx.x == 0) partials[blockIdx.x] = v;
 }
 
@@ -374,6 +402,7 @@ TLH_API int tlh_gradient_squared_norm_multi(const float *const *grads, const uin
                                             void *stream) {
   hipStream_t s = as_stream(stream);
   if (count == 0) return tlh_fill_f32(squared_norm, 0.0f, 1, stream);
+  if (count > kMaxMultiTensors) return int(hipErrorInvalidValue);
   sqnorm_multi_kernel<<<TLH_NORM_PARTIALS, 256, 0, s>>>(grads, sizes, count, partials);
   int st = launch_status();
   if (st) return st;

@@ -453,14 +453,19 @@ def test_gradient_norm_single_and_multi(g):
     g.call("tlh_accumulate_gradient_squared_norm", g.dev(first), 3, s)
     g.call("tlh_accumulate_gradient_squared_norm", g.dev(second), 1, s)
     assert abs(g.host(s)[0] - 169.0) < 1e-5
-    sizes = [384 * 384, 384, 1536 * 384, 1536, 2048 * 384, 7, 1]
-    grads = [g.dev(O.normal((n,), 40 + i)) for i, n in enumerate(sizes)]
-    ptrs = torch.tensor([t.data_ptr() for t in grads], dtype=torch.int64, device="cuda")
+    # 16-byte aligned tensors (float4 path, n % 4 tails) and two that start
+    # one float past an aligned address (scalar path)
+    sizes = [384 * 384, 384, 1536 * 384, 1536, 2048 * 384, 7, 1, 9001, 5]
+    skew = [0, 0, 0, 0, 0, 0, 0, 1, 1]
+    grads = [g.dev(O.normal((n + k,), 40 + i)) for i, (n, k) in enumerate(zip(sizes, skew))]
+    ptrs = torch.tensor([t.data_ptr() + 4 * k for t, k in zip(grads, skew)], dtype=torch.int64,
+                        device="cuda")
     dsz = torch.tensor(sizes, dtype=torch.int64, device="cuda")
     partials = g.empty((1024,))
     out = g.empty((1,))
     g.call("tlh_gradient_squared_norm_multi", ptrs, dsz, len(sizes), partials, out)
-    expect = sum(float((g.host(t).astype(np.float64) ** 2).sum()) for t in grads)
+    expect = sum(float((g.host(t)[k:].astype(np.float64) ** 2).sum())
+                 for t, k in zip(grads, skew))
     assert abs(g.host(out)[0] - expect) / expect < 1e-5
 
 
