@@ -251,6 +251,10 @@ def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
         dw, db = gemm(g, x, dy, ta=True, bias_grad_init=np.zeros(N, np.float32))
         assert_rel(dw.reshape(M, N), O.matmul(x.T, dy), 1e-3, f"dW splits={splits}")
         assert_close(db, O.sum_to_shape(dy, [N]), rtol=1e-4, atol=1e-3, what="db")
+    forced_plan(bm, bn, 1, bk)  # ragged edges (the bounds-checked path)
+    a, b = O.normal((200, 100), 154, 0, 0.5), O.normal((100, 300), 155, 0, 0.5)
+    out, _ = gemm(g, a, b)
+    assert_rel(out.reshape(200, 300), O.matmul(a, b), 1e-3, "ragged")
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
