@@ -116,6 +116,30 @@ int tlg_profile_step(void *program, float root_grad, float max_norm, float *host
  * per-launch time (ms). Rewrites the step's scratch and gradient buffers. */
 int tlg_time_gemms(void *program, uint32_t iters, float *host_ms);
 
+/* Checkpoints in the reference's archive format (include/model_utils/
+ * archive.h, src/model_utils/archive.cpp:9-92), holding what
+ * passes::Compiled::save and save_optimisers write
+ * (include/passes/compile.h:259-299): for each parameter i in the
+ * reference's gradient-path order
+ *   parameters/<i>/size  u32 shape ([in, out] weights, [1, n] biases,
+ *                        [V, D] token and [T, D] position tables)
+ *   parameters/<i>/data  fp32 values
+ * and, with `optimiser` != 0, AdamW's state (include/optimiser/
+ * AdamW.h:84-106)
+ *   optimisers/<i>/momentum1/size|data, optimisers/<i>/momentum2/size|data,
+ *   optimisers/<i>/step  u32.
+ * The order runs over the blocks from the last to the first, each as
+ * w1, b1, w2, b2, wq, bq, wk, bk, wv, bv, wo, bo, then the token and
+ * position tables, then the vocabulary projection wp, bp.
+ * Save and load are synchronous; load checks every shape and size and
+ * leaves the program unchanged on a mismatch (hipErrorInvalidValue). */
+int tlg_save_archive(void *program, const char *path, int optimiser);
+int tlg_load_archive(void *program, const char *path, int optimiser);
+/* Host-only: the canonical parameter index (tlg_param_info order) and the
+ * 2-d shape of archive entry `index` for `cfg`. */
+int tlg_archive_entry(const tlg_config *cfg, uint32_t index, uint32_t *canonical,
+                      uint32_t *shape2);
+
 /* Records tlg_train_step(root_grad, max_norm, 1) as a hipGraph; replays it. */
 int tlg_capture_train_step(void *program, float root_grad, float max_norm);
 int tlg_replay(void *program);

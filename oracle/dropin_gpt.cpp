@@ -194,8 +194,11 @@ Tensors canonical_weights(uint32_t seed) {
   return w;
 }
 
-void anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
-            const std::vector<uint32_t> &targets, uint32_t seed, float max_norm) {
+// Returns, for every executor parameter index, the canonical index of the
+// same tensor (weights matched by value, biases by gradient), -1 if none.
+std::vector<int> anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
+                        const std::vector<uint32_t> &targets, uint32_t seed, float max_norm) {
+  std::vector<int> canonical_of(orc_rt.params0.size(), -1);
   std::printf("-- oracle runtime vs the oracle's hand-derived GPT step (weights matched by value)\n");
   const orc_gpt_config cfg{kVocab, kSeq, kDim, kHeads, kLayers, kBatch, kFfn};
   const uint32_t count = orc_gpt_param_count(&cfg);
@@ -219,7 +222,9 @@ void anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
   int unmatched = 0;
   for (int s : weight_slot) unmatched += ref_of[s] < 0;
   report("weights identified by value (unmatched count)", unmatched, 0);
-  if (unmatched) return;
+  if (unmatched) return canonical_of;
+  for (uint32_t c = 0; c < count; ++c)
+    if (ref_of[c] >= 0) canonical_of[ref_of[c]] = int(c);
   std::vector<float> params, m, v;
   for (uint32_t c = 0; c < count; ++c) {
     const size_t n = orc_gpt_param_size(&cfg, c);
@@ -241,12 +246,16 @@ void anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
   double w_err = 0, b_err = 0;
   size_t off = 0;
   std::vector<std::pair<size_t, std::vector<float>>> bias_grads;
+  std::vector<uint32_t> bias_slot;
   for (uint32_t c = 0; c < count; ++c) {
     const size_t n = orc_gpt_param_size(&cfg, c);
     std::vector<float> g(grads.begin() + off, grads.begin() + off + n);
     for (auto &x : g) x *= clip;
     if (ref_of[c] >= 0) w_err = std::max(w_err, rel_l2(orc_rt.grads[0][ref_of[c]], g));
-    else bias_grads.emplace_back(n, std::move(g));
+    else {
+      bias_grads.emplace_back(n, std::move(g));
+      bias_slot.push_back(c);
+    }
     off += n;
   }
   std::vector<bool> taken(bias_grads.size(), false);
@@ -264,6 +273,7 @@ void anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
       continue;
     }
     taken[best_j] = true;
+    canonical_of[i] = int(bias_slot[best_j]);
     // the key-projection bias has an exactly-zero gradient in exact
     // arithmetic (softmax shift invariance): judge it absolutely
     double scale = 0;
@@ -272,6 +282,33 @@ void anchor(const Outcome &orc_rt, const std::vector<uint32_t> &tokens,
   }
   report("step 1: weight gradients, worst tensor rel-L2", w_err, 1e-4);
   report("step 1: bias gradients (matched by value), worst rel-L2", b_err, 1e-4);
+  return canonical_of;
+}
+
+// The reference checkpoint layout (Compiled::save + save_optimisers,
+// include/passes/compile.h:259-299) of this GPT as JSON: per archive index
+// the tensor shape and the canonical parameter index (the oracle GPT's
+// order). Biases with an exactly-zero gradient (the key projections) match
+// among themselves by first come; they stay zero in training.
+void print_archive_layout(const Outcome &orc_rt, const std::vector<int> &canonical_of) {
+  std::printf("{\"config\": {\"vocab\": %u, \"seq\": %u, \"dim\": %u, \"heads\": %u, "
+              "\"layers\": %u, \"ffn\": %u},\n \"parameters\": [",
+              kVocab, kSeq, kDim, kHeads, kLayers, kFfn);
+  for (size_t i = 0; i < canonical_of.size(); ++i) {
+    const auto &b = orc_rt.archive.at("parameters/" + std::to_string(i) + "/size");
+    std::vector<uint32_t> shape(b.size() / 4);
+    std::memcpy(shape.data(), b.data(), b.size());
+    std::printf("%s\n  {\"shape\": [", i ? "," : "");
+    for (size_t k = 0; k < shape.size(); ++k) std::printf("%s%u", k ? ", " : "", shape[k]);
+    std::printf("], \"canonical\": %d}", canonical_of[i]);
+  }
+  std::printf("],\n \"names\": [");
+  bool first = true;
+  for (const auto &[name, blob] : orc_rt.archive) {
+    std::printf("%s\n  [\"%s\", %zu]", first ? "" : ",", name.c_str(), blob.size());
+    first = false;
+  }
+  std::printf("]}\n");
 }
 
 uint64_t splitmix(uint64_t &s) {
@@ -283,7 +320,7 @@ uint64_t splitmix(uint64_t &s) {
 
 } // namespace
 
-int run(bool cpu_only) {
+int run(bool cpu_only, bool layout) {
   const uint32_t seed = 1;
   const float max_norm = 1.0f;
   std::vector<uint32_t> tokens(kBatch * kSeq), targets(kBatch * kSeq);
@@ -298,7 +335,13 @@ int run(bool cpu_only) {
   orc::Runtime cpu;
   const Outcome ref = train_oracle(cpu, tokens, targets, seed, max_norm);
   std::printf("oracle runtime: loss %.6f -> %.6f\n", ref.losses[0][0], ref.losses[1][0]);
-  anchor(ref, tokens, targets, seed, max_norm);
+  const std::vector<int> canonical_of = anchor(ref, tokens, targets, seed, max_norm);
+  if (layout) {
+    if (g_failures) return 1;
+    std::printf("ARCHIVE LAYOUT\n");
+    print_archive_layout(ref, canonical_of);
+    return 0;
+  }
   if (cpu_only) {
     std::printf("%s\n", g_failures ? "ORACLE ANCHOR FAILED" : "oracle anchor ok");
     return g_failures ? 1 : 0;
@@ -321,12 +364,15 @@ int run(bool cpu_only) {
   return g_failures ? 1 : 0;
 }
 
-// Usage: dropin_gpt [--cpu-only]
+// Usage: dropin_gpt [--cpu-only | --archive-layout]
 //   --cpu-only: only the oracle runtime and its anchor (no GPU needed).
+//   --archive-layout: print the reference checkpoint layout of this GPT as
+//     JSON after "ARCHIVE LAYOUT" (no GPU needed).
 int main(int argc, char **argv) {
   std::setvbuf(stdout, nullptr, _IOLBF, 0);
   try {
-    return run(argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0);
+    const bool layout = argc > 1 && std::strcmp(argv[1], "--archive-layout") == 0;
+    return run(layout || (argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0), layout);
   } catch (const std::exception &e) {
     std::printf("error: %s\n", e.what());
     return 2;

@@ -2,7 +2,10 @@
 // dropin_gpt.cpp). TEST INFRASTRUCTURE ONLY.
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
+#include <map>
+#include <string>
 #include <vector>
 
 namespace hip {
@@ -23,10 +26,13 @@ constexpr int kSteps = 2;
 
 using Tensors = std::vector<std::vector<float>>;
 
+using Blobs = std::map<std::string, std::vector<std::byte>>; // archive name -> bytes
+
 struct Outcome {
   Tensors params0;                        // parameters after prepare()
   std::vector<std::vector<float>> losses; // per step: per-row losses
   std::vector<Tensors> grads, params;     // per step: gradients, updated params
+  Blobs archive; // Compiled::save + save_optimisers after the last step
 };
 
 // src/train.cpp's loop body for kSteps steps of the reference nn::GPT on

@@ -60,6 +60,9 @@ public:
     g_sink->push_back(std::move(h));
     inner_.update(rt, s, p, g, dst);
   }
+  void initialise_for(const T &parameter) { inner_.initialise_for(parameter); }
+  template <typename Arch> void save(Arch &archive) const { inner_.save(archive); }
+  template <typename Arch> void load(Arch &archive) { inner_.load(archive); }
 
 private:
   Optimiser::AdamW<T> inner_;
@@ -104,6 +107,8 @@ Outcome train(Run &rt, const std::vector<uint32_t> &tokens, const std::vector<ui
     compiled.save(archive);
     out.params.push_back(parameters_of(blobs));
   }
+  compiled.save_optimisers(archive);
+  out.archive = blobs;
   return out;
 }
 

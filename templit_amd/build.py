@@ -60,6 +60,7 @@ KERNEL_SOURCES = [
 RUNTIME_SOURCES = [
     "hip_context.cpp",
     "runtime.cpp",
+    "archive.cpp",
 ]
 
 GPT_SOURCES = [
@@ -139,7 +140,7 @@ def build_gpt(kernel_lib: Path) -> Path | None:
     lib = PKG / "libtemplit_gpt.so"
     tmp = PKG / "libtemplit_gpt.so.tmp"
     _run(["g++", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          f"-L{PKG}", "-ltemplit_hip", "-Wl,-rpath,$ORIGIN"])
+          f"-L{PKG}", "-ltemplit_runtime", "-ltemplit_hip", "-Wl,-rpath,$ORIGIN"])
     tmp.replace(lib)
     return lib
 

@@ -21,10 +21,17 @@
 #include "templit_gpt.h"
 #include "templit_hip.h"
 
+#include "model_utils/archive.h"
+
 #include <algorithm>
+#include <array>
+#include <span>
 #include <cmath>
 #include <cstring>
+#include <fstream>
 #include <new>
+#include <stdexcept>
+#include <string>
 #include <vector>
 
 namespace {
@@ -575,6 +582,35 @@ int copy_params(Program &p, float *dev_base, const float *host, bool to_device) 
   return tlh_stream_synchronize(p.stream);
 }
 
+// Archive entry `index` of the reference checkpoint layout (the reference's
+// gradient-path order over nn::GPT: the blocks from the last to the first,
+// each w1 b1 w2 b2 wq bq wk bk wv bv wo bo, then the token and position
+// tables, then wp, bp) -> canonical parameter index and [rows, cols] shape.
+bool archive_entry(const tlg_config &c, uint32_t index, uint32_t &canonical, uint32_t shape[2]) {
+  const uint32_t L = c.layers, D = c.dim, F = c.ffn, V = c.vocab, T = c.seq;
+  static const uint32_t block_slot[12] = {8, 9, 10, 11, 0, 1, 2, 3, 4, 5, 6, 7};
+  const uint32_t last = 2 + 12 * L;
+  if (index < 12 * L) canonical = 2 + 12 * (L - 1 - index / 12) + block_slot[index % 12];
+  else if (index < 12 * L + 4) canonical = std::array<uint32_t, 4>{0, 1, last, last + 1}[index - 12 * L];
+  else return false;
+  if (canonical == 0) shape[0] = V, shape[1] = D;
+  else if (canonical == 1) shape[0] = T, shape[1] = D;
+  else if (canonical == last) shape[0] = D, shape[1] = V;
+  else if (canonical == last + 1) shape[0] = 1, shape[1] = V;
+  else {
+    const uint32_t s = (canonical - 2) % 12;
+    if (s == 8) shape[0] = D, shape[1] = F;       // w1
+    else if (s == 10) shape[0] = F, shape[1] = D; // w2
+    else if (s % 2 == 0) shape[0] = D, shape[1] = D;
+    else shape[0] = 1, shape[1] = (s == 9 ? F : D); // biases
+  }
+  return true;
+}
+
+template <typename T> std::span<const std::byte> bytes_of(const std::vector<T> &v) {
+  return std::as_bytes(std::span<const T>(v));
+}
+
 bool is_bias(const Program &p, uint32_t i) {
   if (i < 2) return false;
   const uint32_t last = 2 + 12 * p.cfg.layers;
@@ -827,6 +863,105 @@ int tlg_time_gemms(void *program, uint32_t iters, float *host_ms) {
   TRY(st);
   *host_ms = total;
   return 0;
+}
+
+int tlg_archive_entry(const tlg_config *cfg, uint32_t index, uint32_t *canonical,
+                      uint32_t *shape2) {
+  if (!cfg || !canonical || !shape2) return kInvalidValue;
+  return archive_entry(*cfg, index, *canonical, shape2) ? 0 : kInvalidValue;
+}
+
+int tlg_save_archive(void *program, const char *path, int optimiser) {
+  Program *p = static_cast<Program *>(program);
+  if (!path) return kInvalidValue;
+  const uint32_t count = uint32_t(p->size.size());
+  std::vector<uint32_t> steps(count);
+  TRY(tlh_stream_synchronize(p->stream));
+  TRY(tlh_memcpy_d2h(steps.data(), p->steps, count * sizeof(uint32_t), p->stream));
+  TRY(tlh_stream_synchronize(p->stream));
+  try {
+    Archive archive;
+    auto params = archive.scope("parameters");
+    auto optimisers = archive.scope("optimisers");
+    for (uint32_t i = 0; i < count; ++i) {
+      uint32_t c = 0;
+      std::vector<uint32_t> shape(2);
+      if (!archive_entry(p->cfg, i, c, shape.data())) return kInvalidValue;
+      std::vector<float> host(p->size[c]);
+      auto put = [&](ArchiveView view, const float *dev) {
+        TRY(tlh_memcpy_d2h(host.data(), dev + p->offset[c], host.size() * sizeof(float),
+                           p->stream));
+        TRY(tlh_stream_synchronize(p->stream));
+        view.write("size", bytes_of(shape));
+        view.write("data", bytes_of(host));
+        return 0;
+      };
+      TRY(put(params.scope(std::to_string(i)), p->params));
+      if (optimiser) {
+        auto state = optimisers.scope(std::to_string(i));
+        TRY(put(state.scope("momentum1"), p->m1));
+        TRY(put(state.scope("momentum2"), p->m2));
+        state.write("step", std::as_bytes(std::span<const uint32_t>(&steps[c], 1)));
+      }
+    }
+    std::ofstream out(path, std::ios::binary | std::ios::trunc);
+    archive.commit(out);
+    out.close();
+    return out.good() ? 0 : kInvalidValue;
+  } catch (const std::exception &) {
+    return kInvalidValue;
+  }
+}
+
+int tlg_load_archive(void *program, const char *path, int optimiser) {
+  Program *p = static_cast<Program *>(program);
+  if (!path) return kInvalidValue;
+  const uint32_t count = uint32_t(p->size.size());
+  // everything is read and checked before anything reaches the device
+  std::vector<float> params(p->total), m1, m2;
+  std::vector<uint32_t> steps(count);
+  if (optimiser) {
+    m1.resize(p->total);
+    m2.resize(p->total);
+  }
+  try {
+    std::ifstream in(path, std::ios::binary);
+    if (!in) return kInvalidValue;
+    Archive archive;
+    archive.restore(in);
+    const auto ps = archive.scope("parameters");
+    const auto os = archive.scope("optimisers");
+    std::vector<size_t> flat(count + 1, 0); // canonical flat offsets
+    for (uint32_t c = 0; c < count; ++c) flat[c + 1] = flat[c] + p->size[c];
+    for (uint32_t i = 0; i < count; ++i) {
+      uint32_t c = 0, want[2];
+      if (!archive_entry(p->cfg, i, c, want)) return kInvalidValue;
+      auto get = [&](const ArchiveView &view, std::vector<float> &dst) {
+        uint32_t shape[2] = {0, 0};
+        view.read("size", std::as_writable_bytes(std::span<uint32_t>(shape, 2)));
+        if (shape[0] != want[0] || shape[1] != want[1])
+          throw std::runtime_error("tensor shape differs from the program's");
+        view.read("data", std::as_writable_bytes(
+                              std::span<float>(dst.data() + flat[c], p->size[c])));
+      };
+      get(ps.scope(std::to_string(i)), params);
+      if (optimiser) {
+        const auto state = os.scope(std::to_string(i));
+        get(state.scope("momentum1"), m1);
+        get(state.scope("momentum2"), m2);
+        state.read("step", std::as_writable_bytes(std::span<uint32_t>(&steps[c], 1)));
+      }
+    }
+  } catch (const std::exception &) {
+    return kInvalidValue;
+  }
+  TRY(copy_params(*p, p->params, params.data(), true));
+  if (optimiser) {
+    TRY(copy_params(*p, p->m1, m1.data(), true));
+    TRY(copy_params(*p, p->m2, m2.data(), true));
+    TRY(tlh_memcpy_h2d(p->steps, steps.data(), count * sizeof(uint32_t), p->stream));
+  }
+  return tlh_stream_synchronize(p->stream);
 }
 
 int tlg_capture_train_step(void *program, float root_grad, float max_norm) {

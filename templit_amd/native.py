@@ -223,7 +223,20 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_time_gemms": [P, c_uint32, POINTER(c_float)],
     "tlg_capture_train_step": [P, c_float, c_float],
     "tlg_replay": [P],
+    "tlg_save_archive": [P, ctypes.c_char_p, c_int],
+    "tlg_load_archive": [P, ctypes.c_char_p, c_int],
+    "tlg_archive_entry": [POINTER(GptConfig), c_uint32, POINTER(c_uint32), POINTER(c_uint32)],
 }
+
+
+def archive_entry(cfg: "GptConfig", index: int) -> tuple[int, tuple[int, int]]:
+    """(canonical parameter index, [rows, cols]) of reference checkpoint entry
+    `index` (host only)."""
+    c = c_uint32()
+    shape = (c_uint32 * 2)()
+    check(load_gpt().tlg_archive_entry(ctypes.byref(cfg), index, ctypes.byref(c), shape),
+          "tlg_archive_entry")
+    return c.value, (shape[0], shape[1])
 
 _GPT: ctypes.CDLL | None = None
 
@@ -401,6 +414,16 @@ class GptProgram:
 
     def replay(self):
         check(self.lib.tlg_replay(self.handle), "replay")
+
+    def save_archive(self, path, optimiser=True):
+        """Checkpoint in the reference's archive format (Compiled::save and,
+        with `optimiser`, save_optimisers)."""
+        check(self.lib.tlg_save_archive(self.handle, str(path).encode(), int(optimiser)),
+              "tlg_save_archive")
+
+    def load_archive(self, path, optimiser=True):
+        check(self.lib.tlg_load_archive(self.handle, str(path).encode(), int(optimiser)),
+              "tlg_load_archive")
 
     def synchronize(self):
         check(load_hip().tlh_stream_synchronize(self.stream), "sync")

@@ -8,13 +8,15 @@ there the checks are size-independent: loss at init ~ ln(V) + s2/2, eager step =
 hipGraph replay (three replays, each checked), and the loss falls when the
 same batch is trained on repeatedly.
 """
+import json
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
 
 import oracle_lib as O
-from templit_amd.native import GptProgram
+from templit_amd.native import GptProgram, NativeError
 
 pytestmark = pytest.mark.gpu
 
@@ -169,6 +171,83 @@ def test_c4_concurrent_weight_gradients_match_serial(c4):
         runs.append((c4.losses(), c4.get_grads(), c4.get_params()))
     for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
         assert np.array_equal(got, want), what
+
+
+def read_archive(path):
+    """name -> bytes of a checkpoint archive file (u32 name length, name,
+    u32 blob length, blob)*."""
+    data, out, i = Path(path).read_bytes(), {}, 0
+    while i + 4 <= len(data):
+        n = int.from_bytes(data[i:i + 4], "little")
+        name = data[i + 4:i + 4 + n].decode()
+        i += 4 + n
+        size = int.from_bytes(data[i:i + 4], "little")
+        out[name] = data[i + 4:i + 4 + size]
+        i += 4 + size
+    return out
+
+
+def test_checkpoint_round_trip_in_the_reference_layout(tmp_path):
+    # the reference GPT's checkpoint (names, sizes, shapes from its own
+    # Compiled::save + save_optimisers); a program that loads it continues
+    # bit-identically to the one that saved it
+    layout = json.loads((Path(__file__).parent / "golden" / "gpt_archive_layout.json").read_text())
+    c = layout["config"]
+    # one head of 64 (the fused attention's head size); the checkpoint holds
+    # no per-head tensors, so its layout does not depend on the head count
+    args = (c["vocab"], c["seq"], c["dim"], c["dim"] // 64, c["layers"], 3)
+    a, b = GptProgram(*args), GptProgram(*args)
+    try:
+        for prog, seed in ((a, 1), (b, 2)):
+            prog.init_params(seed=seed, std=0.05)
+            prog.set_optimizer(**HP)
+            prog.random_batch(seed=9)
+        for _ in range(2):
+            a.train_step(1.0 / a.rows, 1.0)
+        path = tmp_path / "gpt.arc"
+        a.save_archive(path)
+        blobs = read_archive(path)
+        assert {n: len(v) for n, v in blobs.items()} == {n: s for n, s in layout["names"]}
+        for i, entry in enumerate(layout["parameters"]):
+            shape = np.frombuffer(blobs[f"parameters/{i}/size"], np.uint32)
+            assert list(shape) == entry["shape"]
+            assert np.frombuffer(blobs[f"optimisers/{i}/step"], np.uint32)[0] == 2
+        b.load_archive(path)
+        np.testing.assert_array_equal(b.get_params(), a.get_params())
+        for x, y in zip(b.get_moments(), a.get_moments()):
+            np.testing.assert_array_equal(x, y)
+        np.testing.assert_array_equal(b.steps(), a.steps())
+        a.train_step(1.0 / a.rows, 1.0)
+        b.train_step(1.0 / b.rows, 1.0)
+        a.synchronize()
+        b.synchronize()
+        np.testing.assert_array_equal(b.losses(), a.losses())
+        np.testing.assert_array_equal(b.get_params(), a.get_params())
+    finally:
+        a.close()
+        b.close()
+
+
+def test_checkpoint_load_checks_shapes_and_scopes(tmp_path):
+    a = GptProgram(64, 16, 64, 1, 1, 2)
+    wider = GptProgram(64, 16, 128, 2, 1, 2)
+    try:
+        a.init_params(seed=3, std=0.05)
+        a.set_optimizer(**HP)
+        path = tmp_path / "a.arc"
+        a.save_archive(path, optimiser=False)
+        assert not any(n.startswith("optimisers/") for n in read_archive(path))
+        wider.init_params(seed=4, std=0.05)
+        before = wider.get_params()
+        with pytest.raises(NativeError):
+            wider.load_archive(path, optimiser=False)
+        np.testing.assert_array_equal(wider.get_params(), before)  # unchanged
+        with pytest.raises(NativeError):  # no optimiser state in the file
+            a.load_archive(path, optimiser=True)
+        a.load_archive(path, optimiser=False)
+    finally:
+        a.close()
+        wider.close()
 
 
 def test_c4_loss_decreases_on_a_fixed_batch(c4):
