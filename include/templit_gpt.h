@@ -140,6 +140,26 @@ int tlg_load_archive(void *program, const char *path, int optimiser);
 int tlg_archive_entry(const tlg_config *cfg, uint32_t index, uint32_t *canonical,
                       uint32_t *shape2);
 
+/* Host batch -> the program's token and target buffers (batch*seq uint32
+ * ids each, row-major). Synchronous. */
+int tlg_set_batch(void *program, const uint32_t *host_tokens, const uint32_t *host_targets);
+
+/* Token-file loader (src/train.cpp:75-77, 142): Dataset::load_tokens of a
+ * raw uint32 file with the reference's split at `training_fraction`
+ * (src/model_utils/dataset.cpp:16-102) and a Loader over its training
+ * (validation = 0) or validation split seeded with `seed`
+ * (src/model_utils/loader.cpp:5-43); the same batches as the reference's
+ * for one seed. tlg_loader_batch draws the next batch to the host;
+ * tlg_loader_next draws it for a program's (batch, seq) and uploads it
+ * (tlg_set_batch). hipErrorInvalidValue for unreadable files, bad
+ * fractions or sizes. */
+int tlg_loader_open(const char *tokens_path, double training_fraction, int validation,
+                    uint32_t seed, void **loader);
+int tlg_loader_batch(void *loader, uint32_t batch, uint32_t seq, uint32_t *host_inputs,
+                     uint32_t *host_targets);
+int tlg_loader_next(void *loader, void *program);
+int tlg_loader_close(void *loader);
+
 /* Records tlg_train_step(root_grad, max_norm, 1) as a hipGraph; replays it. */
 int tlg_capture_train_step(void *program, float root_grad, float max_norm);
 int tlg_replay(void *program);

@@ -61,6 +61,8 @@ RUNTIME_SOURCES = [
     "hip_context.cpp",
     "runtime.cpp",
     "archive.cpp",
+    "dataset.cpp",
+    "loader.cpp",
 ]
 
 GPT_SOURCES = [

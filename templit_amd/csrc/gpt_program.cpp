@@ -21,7 +21,9 @@
 #include "templit_gpt.h"
 #include "templit_hip.h"
 
+#include "model_utils/Dataset.h"
 #include "model_utils/archive.h"
+#include "model_utils/loader.h"
 
 #include <algorithm>
 #include <array>
@@ -30,6 +32,7 @@
 #include <cstring>
 #include <fstream>
 #include <new>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -611,6 +614,12 @@ template <typename T> std::span<const std::byte> bytes_of(const std::vector<T> &
   return std::as_bytes(std::span<const T>(v));
 }
 
+// A token file's dataset and a loader over one of its splits.
+struct TokenLoader {
+  Dataset dataset;
+  std::optional<Loader> loader;
+};
+
 bool is_bias(const Program &p, uint32_t i) {
   if (i < 2) return false;
   const uint32_t last = 2 + 12 * p.cfg.layers;
@@ -962,6 +971,61 @@ int tlg_load_archive(void *program, const char *path, int optimiser) {
     TRY(tlh_memcpy_h2d(p->steps, steps.data(), count * sizeof(uint32_t), p->stream));
   }
   return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_set_batch(void *program, const uint32_t *host_tokens, const uint32_t *host_targets) {
+  Program *p = static_cast<Program *>(program);
+  if (!host_tokens || !host_targets) return kInvalidValue;
+  TRY(tlh_memcpy_h2d(p->tokens, host_tokens, p->R * sizeof(uint32_t), p->stream));
+  TRY(tlh_memcpy_h2d(p->targets, host_targets, p->R * sizeof(uint32_t), p->stream));
+  return tlh_stream_synchronize(p->stream);
+}
+
+int tlg_loader_open(const char *tokens_path, double training_fraction, int validation,
+                    uint32_t seed, void **loader) {
+  if (!tokens_path || !loader) return kInvalidValue;
+  *loader = nullptr;
+  try {
+    std::ifstream in(tokens_path, std::ios::binary);
+    auto *l = new TokenLoader{Dataset::load_tokens(in, training_fraction), {}};
+    const Dataset &d = l->dataset;
+    l->loader.emplace(validation ? d.validation_split() : d.training_split(), seed);
+    *loader = l;
+    return 0;
+  } catch (const std::exception &) {
+    return kInvalidValue;
+  }
+}
+
+int tlg_loader_batch(void *loader, uint32_t batch, uint32_t seq, uint32_t *host_inputs,
+                     uint32_t *host_targets) {
+  auto *l = static_cast<TokenLoader *>(loader);
+  if (!l || !host_inputs || !host_targets) return kInvalidValue;
+  try {
+    const Loader::Batch &b = l->loader->get_batch(batch, seq);
+    std::copy(b.inputs.begin(), b.inputs.end(), host_inputs);
+    std::copy(b.targets.begin(), b.targets.end(), host_targets);
+    return 0;
+  } catch (const std::exception &) {
+    return kInvalidValue;
+  }
+}
+
+int tlg_loader_next(void *loader, void *program) {
+  auto *l = static_cast<TokenLoader *>(loader);
+  Program *p = static_cast<Program *>(program);
+  if (!l || !p) return kInvalidValue;
+  try {
+    const Loader::Batch &b = l->loader->get_batch(p->cfg.batch, p->cfg.seq);
+    return tlg_set_batch(program, b.inputs.data(), b.targets.data());
+  } catch (const std::exception &) {
+    return kInvalidValue;
+  }
+}
+
+int tlg_loader_close(void *loader) {
+  delete static_cast<TokenLoader *>(loader);
+  return 0;
 }
 
 int tlg_capture_train_step(void *program, float root_grad, float max_norm) {

@@ -226,7 +226,47 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_save_archive": [P, ctypes.c_char_p, c_int],
     "tlg_load_archive": [P, ctypes.c_char_p, c_int],
     "tlg_archive_entry": [POINTER(GptConfig), c_uint32, POINTER(c_uint32), POINTER(c_uint32)],
+    "tlg_set_batch": [P, P, P],
+    "tlg_loader_open": [ctypes.c_char_p, ctypes.c_double, c_int, c_uint32, POINTER(c_void_p)],
+    "tlg_loader_batch": [P, c_uint32, c_uint32, P, P],
+    "tlg_loader_next": [P, P],
+    "tlg_loader_close": [P],
 }
+
+
+class TokenLoader:
+    """Batches of a raw uint32 token file, drawn like the reference's
+    Loader over its Dataset split (host C++ in libtemplit_runtime.so)."""
+
+    def __init__(self, path, training_fraction=0.95, validation=False, seed=1):
+        self.lib = load_gpt()
+        h = c_void_p()
+        check(self.lib.tlg_loader_open(str(path).encode(), training_fraction, int(validation),
+                                       seed, ctypes.byref(h)), "tlg_loader_open")
+        self.handle = h.value
+
+    def batch(self, batch, seq):
+        import numpy as np
+
+        x = np.empty(batch * seq, np.uint32)
+        y = np.empty(batch * seq, np.uint32)
+        check(self.lib.tlg_loader_batch(self.handle, batch, seq, x.ctypes.data, y.ctypes.data),
+              "tlg_loader_batch")
+        return x, y
+
+    def next_into(self, program: "GptProgram"):
+        check(self.lib.tlg_loader_next(self.handle, program.handle), "tlg_loader_next")
+
+    def close(self):
+        if self.handle:
+            self.lib.tlg_loader_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def archive_entry(cfg: "GptConfig", index: int) -> tuple[int, tuple[int, int]]:
@@ -414,6 +454,14 @@ class GptProgram:
 
     def replay(self):
         check(self.lib.tlg_replay(self.handle), "replay")
+
+    def set_batch(self, tokens, targets):
+        np = self._np
+        t = np.ascontiguousarray(tokens, dtype=np.uint32).ravel()
+        y = np.ascontiguousarray(targets, dtype=np.uint32).ravel()
+        if t.size != self.rows or y.size != self.rows:
+            raise ValueError("a batch is batch*seq tokens and targets")
+        check(self.lib.tlg_set_batch(self.handle, t.ctypes.data, y.ctypes.data), "tlg_set_batch")
 
     def save_archive(self, path, optimiser=True):
         """Checkpoint in the reference's archive format (Compiled::save and,

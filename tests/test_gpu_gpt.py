@@ -250,6 +250,43 @@ def test_checkpoint_load_checks_shapes_and_scopes(tmp_path):
         wider.close()
 
 
+def test_token_file_batches_train_the_program():
+    # the loader's next batch lands in the program's token/target buffers
+    # (the same batch a second loader with the seed draws on the host), and
+    # a few steps on the fixture's tokens lower the loss
+    import ctypes
+
+    from templit_amd.native import TokenLoader, check, load_hip
+
+    tokens = Path(__file__).parent / "golden" / "loader_tokens.tokens"
+    prog = GptProgram(2048, 16, 64, 1, 1, 4)
+    feed, host = TokenLoader(tokens, seed=5), TokenLoader(tokens, seed=5)
+    try:
+        prog.init_params(seed=8, std=0.05)
+        prog.set_optimizer(**HP)
+        losses = []
+        for _ in range(6):
+            feed.next_into(prog)
+            x, y = host.batch(4, 16)
+            got = np.empty(prog.rows, np.uint32)
+            check(load_hip().tlh_memcpy_d2h(got.ctypes.data, ctypes.c_void_p(prog.tokens_ptr),
+                                            got.nbytes, ctypes.c_void_p(prog.stream)), "d2h")
+            prog.synchronize()
+            np.testing.assert_array_equal(got, x)
+            prog.train_step(1.0 / prog.rows, 1.0)
+            prog.synchronize()
+            losses.append(float(prog.losses().mean()))
+        assert all(np.isfinite(losses))
+        prog.set_batch(x, y)  # the last batch again: learnt a little
+        prog.train_step(1.0 / prog.rows, 1.0, update=False)
+        prog.synchronize()
+        assert float(prog.losses().mean()) < losses[-1]
+    finally:
+        feed.close()
+        host.close()
+        prog.close()
+
+
 def test_c4_loss_decreases_on_a_fixed_batch(c4):
     c4.init_params(seed=3, std=0.02)
     c4.set_optimizer(lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
