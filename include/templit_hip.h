@@ -359,9 +359,12 @@ int tlh_embedding_add_positions(const float *tok, uint32_t vocab, const float *p
                                 uint32_t seq, uint32_t dim, float *out,
                                 void *stream);
 /* scatter_add_rows (math.metal:794-820, runtime.cpp:952-981): dst[ids[i],:]
- * += values[i,:] with float atomics (order nondeterministic). dst is
- * [dst_rows, dim]; ids >= dst_rows are dropped. The caller pre-fills dst
- * (base copy or zero, runtime.cpp:983-1030). */
+ * += values[i,:]. The reference adds with relaxed float atomics (summation
+ * order varies run to run); here every element receives its contributions
+ * in increasing i, without atomics, so the result is deterministic and
+ * equals the sequential loop bit for bit. dst is [dst_rows, dim]; ids >=
+ * dst_rows are dropped. The caller pre-fills dst (base copy or zero,
+ * runtime.cpp:983-1030). */
 int tlh_scatter_add_rows(const float *values, const uint32_t *ids, size_t n_ids,
                          uint32_t dim, float *dst, uint32_t dst_rows, void *stream);
 /* ---------------------------------------------------------------------------
