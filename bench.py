@@ -4,16 +4,20 @@ config: vocab 2048, T=192, d=384, 4 blocks, 6 heads, FFN 4x, batch 32, fp32,
 CE loss, global grad-norm clip 1.0, AdamW lr 3e-4 b1 0.9 b2 0.95 wd 0.1).
 
 One step = forward + loss + backward + clip + AdamW over one batch of 6,144
-tokens already resident in HBM, replayed as one hipGraph. Prints one JSON
-line: tokens/s, the GEMM roofline fraction (fp32 MFMA), the d=1024 GEMM
-rate, and the CPU oracle's rate on a bounded sample of the same step.
+tokens already resident in HBM, launched eagerly on the program's two
+streams (input gradients on one, weight gradients on the other, ordered by
+events). The same step replayed as one captured hipGraph is timed too and
+reported under "other_execution": on ROCm 7.2 the graph's cross-stream
+edges idle the GPU about 10 us each, so the eager launches are faster.
+Prints one JSON line: tokens/s, the GEMM roofline fraction (fp32 MFMA), the
+d=1024 GEMM rate, and the CPU oracle's rate on a bounded sample of the same
+step.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--graph] [--no-cpu-baseline]
 
-Profiling runs (rocprofv3 counters) use --eager (time eager steps, one
-dispatch per kernel instead of graph replays), --skip-d1024 and
---copy-calibration MiB (one device copy of that size, whose FETCH_SIZE /
-WRITE_SIZE readings scale the counters to bytes).
+Profiling runs (rocprofv3 counters) use --skip-d1024 and --copy-calibration
+MiB (one device copy of that size, whose FETCH_SIZE / WRITE_SIZE readings
+scale the counters to bytes).
 """
 from __future__ import annotations
 
@@ -233,9 +237,23 @@ SCALED = dict(vocab=2048, seq=1024, dim=1024, heads=16, layers=12, batch=8)
 EOS = 256  # the BPE tokeniser's end-of-sequence id (dataset/ tokens split on it)
 
 
+def time_steps(prog, step, warmup: int, steps: int) -> float:
+    """Seconds per step of `steps` calls of `step` after `warmup` untimed ones,
+    bracketed by device synchronisations."""
+    for _ in range(warmup):
+        step()
+    prog.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    prog.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
 def scaled_gpt(steps: int, gen_tokens: int) -> dict:
     """The scaled configuration: d 1024, 16 heads, 12 blocks, T 1024, V 2048,
-    batch 8 -- a training step (hipGraph replay) and greedy generation of
+    batch 8 -- a training step (eager launches on the program's two streams;
+    the hipGraph replay of the same step is timed too) and greedy generation of
     `gen_tokens` tokens from a 32-token random prompt (batch 1, the reference's
     full-window recompute, and the equivalent valid-prefix recompute)."""
     import numpy as np
@@ -249,20 +267,18 @@ def scaled_gpt(steps: int, gen_tokens: int) -> dict:
         prog.init_params(seed=21, std=0.02)
         prog.set_optimizer(**HP)
         prog.random_batch(seed=22)
-        prog.capture(1.0 / tokens, MAX_NORM)
-        for _ in range(2):
-            prog.replay()
-        prog.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            prog.replay()
-        prog.synchronize()
-        dt = (time.perf_counter() - t0) / steps
+        eager = lambda: prog.train_step(1.0 / tokens, MAX_NORM)
+        dt = time_steps(prog, eager, 2, steps)
         model_flops = 6.0 * prog.total * tokens  # excludes attention's T^2 term
         out["train"] = {"tokens_per_step": tokens, "ms_per_step": round(dt * 1e3, 3),
                         "tokens_per_s": round(tokens / dt, 1), "steps": steps,
+                        "execution": "eager launches on two streams",
                         "loss": round(float(prog.losses().mean()), 4),
                         "param_flops_tflops": round(model_flops / dt / 1e12, 2)}
+        prog.capture(1.0 / tokens, MAX_NORM)
+        dt = time_steps(prog, prog.replay, 2, steps)
+        out["train_graph_replay"] = {"ms_per_step": round(dt * 1e3, 3),
+                                     "tokens_per_s": round(tokens / dt, 1)}
     finally:
         prog.close()
     log(f"[bench] scaled train: {out['train']}")
@@ -408,8 +424,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=4)
     ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--graph", action="store_true",
+                    help="time hipGraph replays of the captured step instead of eager launches "
+                         "(the other execution is timed afterwards either way)")
     ap.add_argument("--eager", action="store_true",
-                    help="time eager steps instead of hipGraph replays (for counter runs)")
+                    help="eager launches (the default; kept for existing command lines)")
     ap.add_argument("--skip-d1024", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true",
                     help="skip the single-kernel configurations (matmul+bias, row ops, attention)")
@@ -439,8 +458,9 @@ def main() -> int:
 
     if args.copy_calibration:
         copy_calibration(hip, prog.stream, args.copy_calibration)
-    step = (lambda: prog.train_step(root, MAX_NORM)) if args.eager else prog.replay
-    if not args.eager:
+    eager = lambda: prog.train_step(root, MAX_NORM)
+    step = prog.replay if args.graph else eager
+    if args.graph:
         prog.capture(root, MAX_NORM)
     for _ in range(args.warmup):
         step()
@@ -457,6 +477,16 @@ def main() -> int:
     loss = float(prog.losses().mean())
     log(f"[bench] {args.steps} timed steps: {ms_per_step:.3f} ms/step, "
         f"{tok_s:.0f} tokens/s, loss {loss:.4f}")
+    # the other execution of the same step, for comparison
+    if args.graph:
+        other_name, other = "eager launches on two streams", eager
+    else:
+        other_name, other = "one hipGraph replay per step", prog.replay
+        prog.capture(root, MAX_NORM)
+    other_dt = time_steps(prog, other, args.warmup, args.steps)
+    other_exec = {"execution": other_name, "ms_per_step": round(other_dt * 1e3, 4),
+                  "tokens_per_s": round(tokens / other_dt, 1)}
+    log(f"[bench] {other_name}: {other_exec['ms_per_step']} ms/step")
 
     prof = prog.profile_step(root, MAX_NORM)
     # kernel time: each GEMM launch of that step again, 10 times back to back
@@ -486,8 +516,10 @@ def main() -> int:
                         "vocab 2048, T 192, d 384, 4 blocks, 6 heads, FFN 1536, batch 32",
             "global_batch": CFG["batch"], "seq_len": CFG["seq"], "tokens_per_step": tokens,
             "parallelism": "single GPU",
-            "execution": "eager launches" if args.eager else "one hipGraph replay per step",
+            "execution": "one hipGraph replay per step" if args.graph
+                         else "eager launches on two streams",
         },
+        "other_execution": other_exec,
         "roofline": {
             "bound": "mfma",
             "kernel": "gemm_mfma_kernel (every GEMM launch of one step)",
