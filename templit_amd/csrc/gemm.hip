@@ -553,7 +553,8 @@ constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 //  - otherwise 64x64 tiles with a K tile of 32: 2-4 co-resident blocks per
 //    CU hide the global/LDS latency a single block per CU cannot;
 //  - tall-K products (weight gradients, K = B*T) with too few output tiles
-//    split K so that about 1024 blocks run, each with K chunks of >= 256.
+//    split K so that about 768 blocks (3 per CU) run, each with K chunks of
+//    >= 256 ([384,2048] with K = 6144: 4 splits, 10% faster than 8).
 Plan make_plan(const GemmDesc &d, bool allow_split) {
   // Summed batch entries are one product over the folded K (see gemm_launch).
   const size_t outputs = d.sum_batches ? 1 : size_t(std::max(1, d.batch));
@@ -567,7 +568,7 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
   if (allow_split && one_dim && tiles < size_t(kTargetBlocks) && K >= 2 * kMinSplitK) {
     int splits = 1;
-    while (splits < 16 && tiles * size_t(splits) < 4 * size_t(kTargetBlocks) &&
+    while (splits < 16 && tiles * size_t(splits) < 3 * size_t(kTargetBlocks) &&
            K / (splits * 2) >= kMinSplitK)
       splits *= 2;
     if (splits >= 2) return {64, 64, splits, 32};
