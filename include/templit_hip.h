@@ -266,6 +266,17 @@ int tlh_sum(const float *a, size_t n, float *out, void *stream);
 int tlh_sum_to_shape(const float *a, float *out, uint32_t ndim,
                      const uint32_t *a_shape, const uint32_t *out_shape,
                      void *stream);
+/* Scratch (floats) that tlh_sum_to_shape_ws uses for this reduction; 0 when
+ * it needs none. The tall column sums -- [R, K] -> [1, K] with R >= 256 and
+ * K % 4 == 0, the bias gradients -- split the rows into chunks over about
+ * 1024 blocks and add the chunk partials in chunk order (deterministic). */
+int tlh_sum_to_shape_workspace(uint32_t ndim, const uint32_t *a_shape,
+                               const uint32_t *out_shape, size_t *elems);
+/* tlh_sum_to_shape with that scratch; with less scratch than asked for it
+ * runs the single-pass kernels of tlh_sum_to_shape. */
+int tlh_sum_to_shape_ws(const float *a, float *out, uint32_t ndim,
+                        const uint32_t *a_shape, const uint32_t *out_shape,
+                        float *workspace, size_t workspace_elems, void *stream);
 /* max_to_shape (math.metal:681-714, runtime.cpp:595-659,741-745); same
  * shape rules as tlh_sum_to_shape. */
 int tlh_max_to_shape(const float *a, float *out, uint32_t ndim,

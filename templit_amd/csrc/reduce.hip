@@ -11,6 +11,8 @@
 // block, and the leftover shapes fall back to a thread per output.
 #include "common.h"
 
+#include <algorithm>
+
 #include "../../include/templit_hip.h"
 
 using namespace tlh;
@@ -96,6 +98,65 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const float *__restrict
   }
 }
 
+// ---- tall column sums, two passes (deterministic) -------------------------
+// Pass 1: block (64-column group x, row chunk y) sums its chunk's rows for 64
+// columns -- 16 threads x float4 across the columns, 16 row lanes, the lanes
+// combined in a fixed order -- into partials[chunk][column]. Pass 2 adds each
+// column's chunk partials in chunk order. Spreads [6144, 384] over 16 x 6
+// blocks where one block per 32 columns would use 12 CUs.
+__global__ __launch_bounds__(256) void col_partials_kernel(const float *__restrict__ a,
+                                                           float *__restrict__ partials,
+                                                           size_t rows, uint32_t cols,
+                                                           uint32_t chunk_rows) {
+  __shared__ f4 part[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const uint32_t c = blockIdx.x * 64 + uint32_t(tx) * 4;
+  const size_t r0 = size_t(blockIdx.y) * chunk_rows;
+  const size_t r1 = r0 + chunk_rows < rows ? r0 + chunk_rows : rows;
+  f4 v = {0.f, 0.f, 0.f, 0.f};
+  if (c < cols)
+    for (size_t r = r0 + ty; r < r1; r += 16) v += *reinterpret_cast<const f4 *>(a + r * cols + c);
+  part[ty][tx] = v;
+  __syncthreads();
+  if (ty == 0 && c < cols) {
+    f4 t = part[0][tx];
+#pragma unroll
+    for (int g = 1; g < 16; ++g) t += part[g][tx];
+    *reinterpret_cast<f4 *>(partials + size_t(blockIdx.y) * cols + c) = t;
+  }
+}
+
+__global__ __launch_bounds__(256) void col_finish_kernel(const float *__restrict__ partials,
+                                                         float *__restrict__ out, uint32_t chunks,
+                                                         uint32_t cols, float beta) {
+  for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
+    float t = partials[c];
+    for (uint32_t k = 1; k < chunks; ++k) t += partials[size_t(k) * cols + c];
+    if (beta != 0.0f) t += beta * out[c];
+    out[c] = t;
+  }
+}
+
+// Row chunking of the two-pass column sum: about 1024 blocks, chunks of at
+// least 64 rows (a multiple of 16). chunks == 0: the single-pass kernel fits
+// (few rows, or columns not float4-aligned).
+struct ColSplit {
+  uint32_t chunks = 0, chunk_rows = 0;
+};
+ColSplit col_split(size_t rows, uint32_t cols) {
+  ColSplit cs;
+  if (rows < 256 || cols % 4 != 0) return cs;
+  const size_t groups = (cols + 63) / 64;
+  size_t chunks = std::max<size_t>(1, 1024 / groups);
+  chunks = std::min(chunks, rows / 64);
+  if (chunks < 2) return cs;
+  size_t chunk_rows = (rows + chunks - 1) / chunks;
+  chunk_rows = (chunk_rows + 15) / 16 * 16;
+  cs.chunks = uint32_t((rows + chunk_rows - 1) / chunk_rows);
+  cs.chunk_rows = uint32_t(chunk_rows);
+  return cs;
+}
+
 // ---- general: one thread per output element, serial over reduced dims -----
 struct ReduceLayout {
   int ndim;                 // collapsed rank
@@ -132,34 +193,55 @@ __global__ __launch_bounds__(256) void generic_reduce_kernel(const float *__rest
   }
 }
 
-template <bool MAX>
-int reduce_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a_shape,
-                    const uint32_t *out_shape, void *stream) {
-  if (ndim == 0 || ndim > kMaxDims) return int(hipErrorInvalidValue);
+// A reduction's shape with size-1 dims dropped and runs of equally reduced
+// (or kept) dims merged.
+struct Collapsed {
   size_t n_in = 1, n_out = 1;
+  uint32_t shp[kMaxDims], red[kMaxDims];
+  int nd = 0;
+};
+int collapse(uint32_t ndim, const uint32_t *a_shape, const uint32_t *out_shape, Collapsed &c) {
+  if (ndim == 0 || ndim > kMaxDims) return int(hipErrorInvalidValue);
   for (uint32_t d = 0; d < ndim; ++d) {
     if (out_shape[d] != a_shape[d] && out_shape[d] != 1) return int(hipErrorInvalidValue);
-    n_in *= a_shape[d];
-    n_out *= out_shape[d];
+    c.n_in *= a_shape[d];
+    c.n_out *= out_shape[d];
   }
+  for (uint32_t d = 0; d < ndim; ++d) {
+    if (a_shape[d] == 1) continue;
+    const uint32_t r = out_shape[d] == 1 ? 1u : 0u;
+    if (c.nd > 0 && c.red[c.nd - 1] == r) {
+      c.shp[c.nd - 1] *= a_shape[d];
+    } else {
+      c.shp[c.nd] = a_shape[d];
+      c.red[c.nd] = r;
+      ++c.nd;
+    }
+  }
+  return 0;
+}
+
+// Scratch floats the two-pass column sum needs for this reduction (0: none).
+size_t sum_workspace_elems(const Collapsed &c) {
+  if (c.n_out == 0 || c.n_in == 0 || c.n_in == c.n_out) return 0;
+  if (c.nd != 2 || c.red[0] != 1) return 0;
+  const ColSplit cs = col_split(c.shp[0], c.shp[1]);
+  return size_t(cs.chunks) * c.shp[1];
+}
+
+template <bool MAX>
+int reduce_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a_shape,
+                    const uint32_t *out_shape, float *workspace, size_t workspace_elems,
+                    void *stream) {
+  Collapsed cl;
+  if (const int st = collapse(ndim, a_shape, out_shape, cl)) return st;
+  const size_t n_in = cl.n_in, n_out = cl.n_out;
+  const uint32_t *shp = cl.shp, *red = cl.red;
+  const int nd = cl.nd;
   hipStream_t s = as_stream(stream);
   if (n_out == 0) return 0;
   if (n_in == 0) return tlh_fill_f32(out, MAX ? -INFINITY : 0.0f, n_out, stream);
   if (n_in == n_out) return tlh_copy(a, out, n_in, stream);
-  // Collapse: drop size-1 dims, merge runs of equal reduced/kept status.
-  uint32_t shp[kMaxDims], red[kMaxDims];
-  int nd = 0;
-  for (uint32_t d = 0; d < ndim; ++d) {
-    if (a_shape[d] == 1) continue;
-    const uint32_t r = out_shape[d] == 1 ? 1u : 0u;
-    if (nd > 0 && red[nd - 1] == r) {
-      shp[nd - 1] *= a_shape[d];
-    } else {
-      shp[nd] = a_shape[d];
-      red[nd] = r;
-      ++nd;
-    }
-  }
   // nd >= 1 because n_in != n_out implies some dim > 1 is reduced.
   if (nd == 1) { // everything reduced
     if (MAX) {
@@ -177,6 +259,16 @@ int reduce_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a
     return launch_status();
   }
   if (nd == 2 && red[0] == 1) { // [R, K]: columns
+    const ColSplit cs = MAX ? ColSplit{} : col_split(shp[0], shp[1]);
+    const bool aligned = (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+    if (cs.chunks && aligned && workspace && workspace_elems >= size_t(cs.chunks) * shp[1]) {
+      col_partials_kernel<<<dim3(ceil_div(shp[1], 64), cs.chunks), 256, 0, s>>>(
+          a, workspace, shp[0], shp[1], cs.chunk_rows);
+      if (const int st = launch_status()) return st;
+      col_finish_kernel<<<ceil_div(shp[1], 256), 256, 0, s>>>(workspace, out, cs.chunks, shp[1],
+                                                               0.0f);
+      return launch_status();
+    }
     col_reduce_kernel<MAX><<<ceil_div(shp[1], 32), 256, 0, s>>>(a, out, shp[0], shp[1], 0.0f);
     return launch_status();
   }
@@ -366,12 +458,28 @@ TLH_API int tlh_sum(const float *a, size_t n, float *out, void *stream) {
 
 TLH_API int tlh_sum_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a_shape,
                              const uint32_t *out_shape, void *stream) {
-  return reduce_to_shape<false>(a, out, ndim, a_shape, out_shape, stream);
+  return reduce_to_shape<false>(a, out, ndim, a_shape, out_shape, nullptr, 0, stream);
+}
+
+TLH_API int tlh_sum_to_shape_workspace(uint32_t ndim, const uint32_t *a_shape,
+                                       const uint32_t *out_shape, size_t *elems) {
+  if (!elems) return int(hipErrorInvalidValue);
+  Collapsed cl;
+  if (const int st = collapse(ndim, a_shape, out_shape, cl)) return st;
+  *elems = sum_workspace_elems(cl);
+  return 0;
+}
+
+TLH_API int tlh_sum_to_shape_ws(const float *a, float *out, uint32_t ndim, const uint32_t *a_shape,
+                                const uint32_t *out_shape, float *workspace,
+                                size_t workspace_elems, void *stream) {
+  return reduce_to_shape<false>(a, out, ndim, a_shape, out_shape, workspace, workspace_elems,
+                                stream);
 }
 
 TLH_API int tlh_max_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a_shape,
                              const uint32_t *out_shape, void *stream) {
-  return reduce_to_shape<true>(a, out, ndim, a_shape, out_shape, stream);
+  return reduce_to_shape<true>(a, out, ndim, a_shape, out_shape, nullptr, 0, stream);
 }
 
 TLH_API int tlh_argmax(const float *a, size_t n, uint32_t *out_index, void *stream) {

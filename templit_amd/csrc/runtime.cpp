@@ -479,7 +479,20 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
     if (in(a) != out(o)) check(tlh_copy(in(a), out(o), o.numel(), stream()), "sum_to_shape");
     return;
   }
-  check(tlh_sum_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(), stream()),
+  size_t ws_elems = 0;
+  check(tlh_sum_to_shape_workspace(uint32_t(as.size()), as.data(), aligned.data(), &ws_elems),
+        "sum_to_shape");
+  if (ws_elems == 0) {
+    check(tlh_sum_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(),
+                           stream()),
+          "sum_to_shape");
+    return;
+  }
+  // Row-chunk partials of a tall column sum; freed to the pool right away,
+  // which is safe because its next user is ordered after this work.
+  Tensor partials({uint32_t(ws_elems)});
+  check(tlh_sum_to_shape_ws(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(),
+                            out(partials), ws_elems, stream()),
         "sum_to_shape");
 }
 

@@ -108,6 +108,8 @@ HIP_SIGNATURES: dict[str, list] = {
     # reductions
     "tlh_sum": [P, c_size_t, P, P],
     "tlh_sum_to_shape": [P, P, c_uint32, U32P, U32P, P],
+    "tlh_sum_to_shape_workspace": [c_uint32, U32P, U32P, P],
+    "tlh_sum_to_shape_ws": [P, P, c_uint32, U32P, U32P, P, c_size_t, P],
     "tlh_max_to_shape": [P, P, c_uint32, U32P, U32P, P],
     "tlh_argmax": [P, c_size_t, P, P],
     "tlh_argmax_rows": [P, c_size_t, c_uint32, P, P],

@@ -409,6 +409,49 @@ def test_sum_to_shape(g, shape, target):
     assert_close(g.host(out).reshape(target), O.sum_to_shape(x, target), rtol=1e-4, atol=1e-4)
 
 
+# Tall column sums (bias gradients) take row-chunk partials in a workspace;
+# the others need none and run the single-pass kernels.
+TWO_PASS = [
+    ((32, 192, 384), [1, 1, 384], True), ((6144, 2048), [1, 2048], True),
+    ((300, 1536), [1, 1536], True),      # last chunk shorter than the rest
+    ((8192, 4096), [1, 4096], True),     # d = 1024 FFN bias gradient
+    ((6144, 386), [1, 386], False),      # columns not float4-aligned
+    ((200, 384), [1, 384], False),       # too few rows to split
+    ((32, 192, 384), [32, 192, 1], False),
+]
+
+
+@pytest.mark.parametrize("shape,target,split", TWO_PASS)
+def test_sum_to_shape_workspace(g, shape, target, split):
+    x = O.normal(shape, 33)
+    al = O.aligned_shape(shape, target)
+    elems = ctypes.c_size_t(123)
+    check(g.lib.tlh_sum_to_shape_workspace(len(shape), u32(shape), u32(al), ctypes.byref(elems)),
+          "workspace")
+    assert (elems.value > 0) == split
+    # float64 sums: at 8192 rows the float32 sequential oracle's own rounding
+    # reaches the tolerance on near-zero sums
+    axes = tuple(d for d in range(len(shape)) if al[d] == 1 and shape[d] != 1)
+    want = x.astype(np.float64).sum(axis=axes, keepdims=True).reshape(target)
+    ws = g.empty((max(1, elems.value),))
+    xd = g.dev(x)
+    outs = []
+    for _ in range(2):
+        out = g.empty(al)
+        g.call("tlh_sum_to_shape_ws", xd, out, len(shape), u32(shape), u32(al), ws, elems.value)
+        outs.append(g.host(out))
+    assert_close(outs[0].reshape(target), want, rtol=1e-4, atol=1e-4)
+    np.testing.assert_array_equal(outs[0], outs[1])  # deterministic
+    rows = x.size // int(np.prod(target))
+    # too little scratch: the single-pass kernel (its per-thread sequential
+    # float32 sums drift past atol 1e-4 beyond ~6k rows; the two-pass ones do not)
+    if split and rows <= 6144:
+        out = g.empty(al)
+        g.call("tlh_sum_to_shape_ws", xd, out, len(shape), u32(shape), u32(al), ws,
+               elems.value - 1)
+        assert_close(g.host(out).reshape(target), want, rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("shape,target", [((2, 3), [2, 1]), ((32, 6, 192, 192), [32, 6, 192, 1]),
                                           ((7, 9, 5), [1, 9, 5]), ((4, 5, 6), [4, 1, 6])])
 def test_max_to_shape(g, shape, target):
