@@ -242,6 +242,25 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ a
   }
 }
 
+// Permutations that keep the last dimension contiguous (head split/merge,
+// [B,T,H,D] <-> [B,H,T,D]): one float4 per thread, 32-bit index math. G is
+// in float4 units (last extent and every stride divided by 4).
+__global__ __launch_bounds__(256) void gather4_kernel(const f4 *__restrict__ a,
+                                                      f4 *__restrict__ out, uint32_t n4,
+                                                      Gather G) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    uint32_t rem = i;
+    size_t off = 0;
+    for (int d = G.ndim - 1; d >= 0; --d) {
+      const uint32_t c = rem % uint32_t(G.shape[d]);
+      rem /= uint32_t(G.shape[d]);
+      off += size_t(c) * G.in_strides[d];
+    }
+    out[i] = a[off];
+  }
+}
+
 // Batched 2-D transpose through a padded 64x64 LDS tile:
 // out[z, i, j] = a[z*batch_stride + j*ld_in + i] with out [z, rows, cols]
 // row-major (rows = input columns).
@@ -363,6 +382,17 @@ TLH_API int tlh_transpose(const float *a, float *out, uint32_t ndim, const uint3
   for (uint32_t d = 0; d < ndim; ++d) {
     G.shape[d] = out_shape[d];
     G.in_strides[d] = in_strides[d];
+  }
+  bool vec = in_strides[ndim - 1] == 1 && out_shape[ndim - 1] % 4 == 0 && aligned16(a) &&
+             aligned16(out) && n / 4 <= 0xffffffffull;
+  for (uint32_t d = 0; d + 1 < ndim && vec; ++d) vec = in_strides[d] % 4 == 0;
+  if (vec) {
+    G.shape[ndim - 1] /= 4;
+    for (uint32_t d = 0; d + 1 < ndim; ++d) G.in_strides[d] /= 4;
+    const uint32_t n4 = uint32_t(n / 4);
+    gather4_kernel<<<stride_grid(n4, 256), 256, 0, s>>>(reinterpret_cast<const f4 *>(a),
+                                                       reinterpret_cast<f4 *>(out), n4, G);
+    return launch_status();
   }
   gather_kernel<<<stride_grid(n, 256), 256, 0, s>>>(a, out, n, G);
   return launch_status();

@@ -549,7 +549,10 @@ constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 // Tile plan, from measurements on MI355X of the GPT step's shapes
 // (M, N, K in {384, 1536, 2048, 6144}) and the d=1024 shapes:
 //  - 128x128 tiles (K tile 16) only when they give every CU three or more
-//    blocks; their 4 accumulators per wave win when the grid is deep;
+//    blocks and pad the output little more than 64x64 tiles do (192x192
+//    attention scores: 4 tiles of 128 cover 1.8x the area, 9 of 64 exactly,
+//    and run 2x faster); their 4 accumulators per wave win when the grid is
+//    deep;
 //  - otherwise 64x64 tiles with a K tile of 32: 2-4 co-resident blocks per
 //    CU hide the global/LDS latency a single block per CU cannot;
 //  - tall-K products (weight gradients, K = B*T) with too few output tiles
@@ -564,7 +567,14 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
     const bool can_split = allow_split && one_dim;
     return {g_force_bm, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, g_force_bk};
   }
-  if (tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks)) return {128, 128, 1, 16};
+  // output area over the area of the tiles that cover it
+  auto coverage = [&](int bm, int bn) {
+    return double(d.M) * double(d.N) /
+           (double((d.M + bm - 1) / bm * bm) * double((d.N + bn - 1) / bn * bn));
+  };
+  if (tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
+      coverage(128, 128) >= 0.9 * coverage(64, 64))
+    return {128, 128, 1, 16};
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
   if (allow_split && one_dim && tiles < size_t(kTargetBlocks) && K >= 2 * kMinSplitK) {
     int splits = 1;

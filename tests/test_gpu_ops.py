@@ -95,7 +95,9 @@ def test_gelu_backward(g):
 
 
 TRANSPOSES = [((6144, 1536), -2, -1), ((32, 192, 6, 64), 1, 2), ((32, 6, 192, 64), -2, -1),
-              ((4, 100, 70), -2, -1), ((3, 4, 5, 6), 0, 3), ((1, 384), 0, 1)]
+              ((4, 100, 70), -2, -1), ((3, 4, 5, 6), 0, 3), ((1, 384), 0, 1),
+              ((32, 6, 192, 64), 0, 1), ((2, 3, 5, 4, 8), 1, 3),  # float4 gathers
+              ((4, 5, 6), 0, 1)]                                  # last dim not float4
 
 
 @pytest.mark.parametrize("shape,da,db", TRANSPOSES)
