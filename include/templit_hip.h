@@ -269,7 +269,7 @@ int tlh_sum_to_shape(const float *a, float *out, uint32_t ndim,
 /* Scratch (floats) that tlh_sum_to_shape_ws uses for this reduction; 0 when
  * it needs none. The tall column sums -- [R, K] -> [1, K] with R >= 256 and
  * K % 4 == 0, the bias gradients -- split the rows into chunks over about
- * 1024 blocks and add the chunk partials in chunk order (deterministic). */
+ * 512 blocks and add the chunk partials in a fixed order (deterministic). */
 int tlh_sum_to_shape_workspace(uint32_t ndim, const uint32_t *a_shape,
                                const uint32_t *out_shape, size_t *elems);
 /* tlh_sum_to_shape with that scratch; with less scratch than asked for it

@@ -102,8 +102,8 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const float *__restrict
 // Pass 1: block (64-column group x, row chunk y) sums its chunk's rows for 64
 // columns -- 16 threads x float4 across the columns, 16 row lanes, the lanes
 // combined in a fixed order -- into partials[chunk][column]. Pass 2 adds each
-// column's chunk partials in chunk order. Spreads [6144, 384] over 16 x 6
-// blocks where one block per 32 columns would use 12 CUs.
+// column's chunk partials in a fixed order (col_finish_kernel). Spreads [6144, 384]
+// over 6 x 48 blocks where one block per 32 columns would use 12 CUs.
 __global__ __launch_bounds__(256) void col_partials_kernel(const float *__restrict__ a,
                                                            float *__restrict__ partials,
                                                            size_t rows, uint32_t cols,
@@ -126,19 +126,28 @@ __global__ __launch_bounds__(256) void col_partials_kernel(const float *__restri
   }
 }
 
-__global__ __launch_bounds__(256) void col_finish_kernel(const float *__restrict__ partials,
-                                                         float *__restrict__ out, uint32_t chunks,
-                                                         uint32_t cols, float beta) {
-  for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
-    float t = partials[c];
-    for (uint32_t k = 1; k < chunks; ++k) t += partials[size_t(k) * cols + c];
-    if (beta != 0.0f) t += beta * out[c];
-    out[c] = t;
+// Pass 2 keeps 8 chunk loads in flight per column: accumulator j takes
+// chunks j, j + 8, ..., and the accumulators are added in j order.
+__global__ __launch_bounds__(64) void col_finish_kernel(const float *__restrict__ partials,
+                                                        float *__restrict__ out, uint32_t chunks,
+                                                        uint32_t cols, float beta) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (uint32_t k0 = 0; k0 < chunks; k0 += 8) {
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (k0 + j < chunks) acc[j] += partials[size_t(k0 + j) * cols + c];
   }
+  float t = acc[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) t += acc[j];
+  if (beta != 0.0f) t += beta * out[c];
+  out[c] = t;
 }
 
-// Row chunking of the two-pass column sum: about 1024 blocks, chunks of at
-// least 64 rows (a multiple of 16). chunks == 0: the single-pass kernel fits
+// Row chunking of the two-pass column sum: about 512 blocks, chunks of at
+// least 128 rows (a multiple of 16). chunks == 0: the single-pass kernel fits
 // (few rows, or columns not float4-aligned).
 struct ColSplit {
   uint32_t chunks = 0, chunk_rows = 0;
@@ -146,9 +155,10 @@ struct ColSplit {
 ColSplit col_split(size_t rows, uint32_t cols) {
   ColSplit cs;
   if (rows < 256 || cols % 4 != 0) return cs;
+  // (rows >= 256 gives at least 2 chunks of 128 rows below)
   const size_t groups = (cols + 63) / 64;
-  size_t chunks = std::max<size_t>(1, 1024 / groups);
-  chunks = std::min(chunks, rows / 64);
+  size_t chunks = std::max<size_t>(1, 512 / groups);
+  chunks = std::min(chunks, rows / 128);
   if (chunks < 2) return cs;
   size_t chunk_rows = (rows + chunks - 1) / chunks;
   chunk_rows = (chunk_rows + 15) / 16 * 16;
@@ -265,8 +275,8 @@ int reduce_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a
       col_partials_kernel<<<dim3(ceil_div(shp[1], 64), cs.chunks), 256, 0, s>>>(
           a, workspace, shp[0], shp[1], cs.chunk_rows);
       if (const int st = launch_status()) return st;
-      col_finish_kernel<<<ceil_div(shp[1], 256), 256, 0, s>>>(workspace, out, cs.chunks, shp[1],
-                                                               0.0f);
+      col_finish_kernel<<<ceil_div(shp[1], 64), 64, 0, s>>>(workspace, out, cs.chunks, shp[1],
+                                                             0.0f);
       return launch_status();
     }
     col_reduce_kernel<MAX><<<ceil_div(shp[1], 32), 256, 0, s>>>(a, out, shp[0], shp[1], 0.0f);
