@@ -250,7 +250,8 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * automatic plan. Process-wide, for measurement sweeps. A forced split
  * count needs a workspace sized for it (tlh_gemm_workspace_size).
  * bk = -1 / -2 instead switches the XCD-aware block order off / on
- * (default on), bk = -3 / -4 the tail split off / on (default on); both
+ * (default on), bk = -3 / -4 the tail split off / on (default on),
+ * bk = -5 / -6 the rectangular XCD tile blocks off / on (default on); these
  * leave the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 

@@ -48,6 +48,10 @@ struct GemmParams {
   int k_chunk;
   int tiles_n;
   int xcd_remap;
+  // XCD rectangles (0 = off): XCD j takes the rect_m x rect_n tile block at
+  // ((j / py) * rect_m, (j % py) * rect_n), py = tiles_n / rect_n; 8 blocks
+  // tile the grid exactly. Set only without a tail split.
+  int rect_m, rect_n;
   uint32_t bias_bstride; // bias (and bias-gradient) elements between batch entries
   int batch;             // output entries (blockIdx.z = entry * splits + split)
   // K-segmented operands (summed batch entries): K index k lies in segment
@@ -102,13 +106,22 @@ template <int BM, int BN>
 __device__ inline BlockCtx block_ctx(const GemmParams &p) {
   BlockCtx b;
   // Blocks are dispatched round-robin over the 8 XCDs (block x runs on XCD
-  // x % 8), each with its own L2. Give XCD j the contiguous tile range
-  // [j*G/8, (j+1)*G/8): tiles of the same tile row then share their A rows
-  // (and neighbouring rows their B columns) in one L2.
+  // x % 8), each with its own L2. Give XCD j a block of tiles that share
+  // operand panels in its L2: a rectangle of the tile grid (rows share A
+  // rows, columns share B columns) when the host found one that needs fewer
+  // panels, else the contiguous tile range [j*G/8, (j+1)*G/8).
   const int bx = int(blockIdx.x);
   b.partial = p.tail_splits > 0 && bx >= p.dp_tiles;
   const int nblk = p.tail_splits > 0 ? p.dp_tiles : int(gridDim.x);
-  int tile = (p.xcd_remap && (nblk & 7) == 0) ? (bx & 7) * (nblk >> 3) + (bx >> 3) : bx;
+  int tile;
+  if (p.rect_m > 0) {
+    const int xcd = bx & 7, i = bx >> 3, py = p.tiles_n / p.rect_n;
+    const int tm = (xcd / py) * p.rect_m + i / p.rect_n;
+    const int tn = (xcd % py) * p.rect_n + i % p.rect_n;
+    tile = tm * p.tiles_n + tn;
+  } else {
+    tile = (p.xcd_remap && (nblk & 7) == 0) ? (bx & 7) * (nblk >> 3) + (bx >> 3) : bx;
+  }
   int tail = 0, tail_split = 0;
   if (b.partial) {
     tail = (bx - p.dp_tiles) / p.tail_splits;
@@ -543,6 +556,36 @@ constexpr int kTargetBlocks = 256; // one block per CU at least
 // planner decides.
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
 int g_xcd_remap = 1;
+int g_xcd_rects = 1;
+
+// The 8-way partition of a tiles_m x tiles_n grid into equal rectangles
+// (1x8, 2x4, 4x2 or 8x1 of them) whose rectangle needs the fewest operand
+// panels (rect_m A row panels + rect_n B column panels), used when it needs
+// fewer than the contiguous range of the same size, which spans
+// ceil(G/8 / tiles_n) tile rows (one more when it starts mid-row) and up to
+// tiles_n columns. {0, 0}: none.
+struct XcdRect {
+  int rect_m = 0, rect_n = 0;
+};
+XcdRect xcd_rect(int tiles_m, int tiles_n) {
+  XcdRect best;
+  const long tiles = long(tiles_m) * tiles_n;
+  if (tiles_m <= 0 || tiles_n <= 0 || tiles % 8 != 0) return best;
+  const long per = tiles / 8;
+  const long rows = (per + tiles_n - 1) / tiles_n + (per % tiles_n ? 1 : 0);
+  long best_cost = std::min<long>(rows, tiles_m) + std::min<long>(per, tiles_n);
+  for (int px = 1; px <= 8; px *= 2) {
+    const int py = 8 / px;
+    if (tiles_m % px || tiles_n % py) continue;
+    const long cost = tiles_m / px + tiles_n / py;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best.rect_m = tiles_m / px;
+      best.rect_n = tiles_n / py;
+    }
+  }
+  return best;
+}
 int g_tail_split = 1;
 constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 
@@ -722,6 +765,12 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.tail_tiles = ts.tails;
   p.tail_splits = ts.splits;
   p.tail_k_chunk = ts.k_chunk;
+  p.rect_m = p.rect_n = 0;
+  if (p.xcd_remap && g_xcd_rects && !ts.splits) {
+    const XcdRect r = xcd_rect(tiles_m, p.tiles_n);
+    p.rect_m = r.rect_m;
+    p.rect_n = r.rect_n;
+  }
   if (K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
     gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
@@ -806,13 +855,18 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
 
 TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   // bk < 0 toggles instead: the XCD-aware block order off (-1) or on (-2),
-  // the tail split off (-3) or on (-4).
+  // the tail split off (-3) or on (-4), the XCD rectangles off (-5) or on
+  // (-6).
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
     return 0;
   }
   if (bk == -3 || bk == -4) {
     tlh::g_tail_split = bk == -4;
+    return 0;
+  }
+  if (bk == -5 || bk == -6) {
+    tlh::g_xcd_rects = bk == -6;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));

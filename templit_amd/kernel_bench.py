@@ -272,12 +272,16 @@ def main() -> int:
     ap.add_argument("--only", help="GEMM shapes whose name contains this text")
     ap.add_argument("--no-tail-split", action="store_true",
                     help="no K-chunked tail tiles for grids that do not spread evenly")
+    ap.add_argument("--no-xcd-rects", action="store_true",
+                    help="contiguous tile ranges per XCD instead of rectangular tile blocks")
     args = ap.parse_args()
     if not (args.gemm or args.attention or args.memory):
         args.gemm = args.attention = args.memory = True
     b = Bench()
     if args.no_tail_split:
         check(b.hip.tlh_gemm_set_plan(0, 0, 0, -3), "plan")
+    if args.no_xcd_rects:
+        check(b.hip.tlh_gemm_set_plan(0, 0, 0, -5), "plan")
     try:
         if args.copy_calibration:
             n = args.copy_calibration * (1 << 20) // 4

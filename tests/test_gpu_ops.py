@@ -230,6 +230,23 @@ def forced_plan(g):
     yield lambda *plan: check(g.lib.tlh_gemm_set_plan(*plan), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, 16), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -4), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -6), "set_plan")
+
+
+@pytest.mark.parametrize("M,N,K,ta", [(384, 2048, 6144, True), (384, 1536, 6144, True),
+                                      (6144, 2048, 384, False), (2048, 1024, 256, False)])
+def test_gemm_xcd_rectangles(g, forced_plan, M, N, K, ta):
+    # The XCD rectangles change which block computes a tile, not how it is
+    # computed: the results are bitwise equal to the contiguous block order.
+    a = O.normal((K, M) if ta else (M, K), 40, 0, 0.5)
+    b = O.normal((K, N), 41, 0, 0.5)
+    outs = []
+    for toggle in (-6, -5):
+        forced_plan(0, 0, 0, toggle)
+        out, _ = gemm(g, a, b, ta, False)
+        outs.append(out)
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert_rel(outs[0].reshape(M, N), O.matmul(a.T if ta else a, b), 1e-3, "gemm")
 
 
 @pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
