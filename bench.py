@@ -254,8 +254,9 @@ def scaled_gpt(steps: int, gen_tokens: int) -> dict:
     """The scaled configuration: d 1024, 16 heads, 12 blocks, T 1024, V 2048,
     batch 8 -- a training step (eager launches on the program's two streams;
     the hipGraph replay of the same step is timed too) and greedy generation of
-    `gen_tokens` tokens from a 32-token random prompt (batch 1, the reference's
-    full-window recompute, and the equivalent valid-prefix recompute)."""
+    `gen_tokens` tokens from a 32-token random prompt (batch 1: the reference's
+    full-window recompute, the equivalent valid-prefix recompute, and a KV
+    cache that runs each new position alone)."""
     import numpy as np
 
     from templit_amd.native import GptProgram
@@ -287,7 +288,7 @@ def scaled_gpt(steps: int, gen_tokens: int) -> dict:
         gen.init_params(seed=21, std=0.02)
         prompt = np.random.default_rng(23).integers(0, SCALED["vocab"], 32, dtype=np.uint32)
         gen.generate_greedy(prompt, 2, EOS)  # warm-up
-        for mode, prefix in (("full_window", False), ("valid_prefix", True)):
+        for mode, prefix in (("full_window", 0), ("valid_prefix", 1), ("kv_cache", 2)):
             t0 = time.perf_counter()
             toks = gen.generate_greedy(prompt, gen_tokens, EOS, prefix_only=prefix)
             dt = time.perf_counter() - t0
@@ -296,7 +297,8 @@ def scaled_gpt(steps: int, gen_tokens: int) -> dict:
                                        "first_tokens": [int(t) for t in toks[:8]]}
     finally:
         gen.close()
-    log(f"[bench] scaled generation: {out['generate_full_window']}, {out['generate_valid_prefix']}")
+    log(f"[bench] scaled generation: {out['generate_full_window']}, {out['generate_valid_prefix']}, "
+        f"{out['generate_kv_cache']}")
     return out
 
 

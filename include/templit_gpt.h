@@ -90,7 +90,12 @@ int tlg_forward(void *program);
  * (sliding the window once full) and stores it in host_out[step]; EOS does
  * not end generation. prefix_only = 0 recomputes the whole padded window
  * as the reference does; 1 computes only the valid prefix, which gives the
- * same logits because attention is causal. Synchronous. */
+ * same logits because attention is causal; 2 keeps the window's keys and
+ * values (KV cache): after one window forward each new position runs alone
+ * through the blocks (tlh_attention_decode over the cached keys) until the
+ * window is full, then it recomputes as 0 does. Modes 1 and 2 compute the
+ * same quantities as 0 in a different order, so their logits agree with
+ * mode 0's to rounding. Synchronous. */
 int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
                         uint32_t n_new, uint32_t eos_token, int prefix_only,
                         uint32_t *host_out);

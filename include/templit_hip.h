@@ -214,7 +214,9 @@ typedef struct tlh_gemm_desc {
   float beta;
   int32_t epilogue;
   /* if remap_h > 0: element (m = b*remap_t + t, n = h*remap_d + d) is stored
-   * at ((b*remap_h + h)*remap_t + t)*remap_d + d */
+   * at ((b*remap_h + h)*remap_t + t)*remap_d + d. M is a multiple of
+   * remap_t (whole sequences) or at most remap_t (rows of one sequence; c
+   * may point t0 rows into the planes to store rows t0.. of a sequence). */
   int32_t remap_t, remap_h, remap_d;
   /* if non-NULL: bias_grad[n] = beta*bias_grad[n] + sum_k op(B)[k][n]. For a
    * weight gradient C = X^T.dY this is the bias gradient (the reference's
@@ -394,6 +396,14 @@ int tlh_attention_forward(const float *q, const float *k, const float *v,
                           float *o, float *lse, uint32_t batch, uint32_t heads,
                           uint32_t seq, uint32_t head_dim, float scale,
                           int causal, int o_merged, void *stream);
+/* Single-query causal attention for incremental decoding: the query of
+ * position t attends to keys 0..t (no reference op: the reference recomputes
+ * the whole window per token, include/inference.h:70-98). q, k, v are
+ * [heads, t_stride, 64] planes -- the forward's head layout at batch 1 --
+ * and o is [heads * 64] (heads merged). t < t_stride <= 8192; head_dim 64. */
+int tlh_attention_decode(const float *q, const float *k, const float *v, float *o,
+                         uint32_t heads, uint32_t t_stride, uint32_t t,
+                         uint32_t head_dim, float scale, void *stream);
 /* Backward. do_ and o in the same layout as the forward's o (o_merged);
  * dq, dk, dv: [B, H, T, D] unless dqkv_merged != 0, then [B, T, H*D].
  * `delta` is scratch [B, H, T]. */

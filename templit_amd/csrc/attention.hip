@@ -504,7 +504,88 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
                      active && half == 0);
 }
 
+// ---- single-query decode ----------------------------------------------------
+// The query of position t attends to keys 0..t of the K/V planes
+// ([heads][t_stride][64], the forward's head layout at batch 1): o[h*64 + d].
+// Block per head, 256 threads: one key per thread for the scores (kept in
+// LDS), block max and sum, then o = sum_j p_j v_j / l with the threads as 16
+// key groups x 16 float4 columns (coalesced rows of V, 8 loads in flight per
+// thread), the groups added in a fixed order.
+constexpr uint32_t kDecodeMaxT = 8192;
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ q,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          float *__restrict__ o,
+                                                          uint32_t t_stride, uint32_t t,
+                                                          float scale) {
+  extern __shared__ float sm[];
+  float *score = sm;                           // t + 1 scores
+  f4 *part = reinterpret_cast<f4 *>(sm + ((t + 1 + 3) & ~3u)); // [16][16] partial sums
+  float *red = reinterpret_cast<float *>(part + 16 * 16);        // reduction scratch
+  const size_t plane = size_t(blockIdx.x) * t_stride * HD;
+  const f4 *qh = reinterpret_cast<const f4 *>(q + plane + size_t(t) * HD);
+  const float *kh = k + plane, *vh = v + plane;
+  f4 qr[HD / 4];
+#pragma unroll
+  for (int i = 0; i < HD / 4; ++i) qr[i] = qh[i];
+  float mx = -INFINITY;
+  for (uint32_t j = threadIdx.x; j <= t; j += blockDim.x) {
+    const f4 *kj = reinterpret_cast<const f4 *>(kh + size_t(j) * HD);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+      const f4 kv = kj[i];
+      acc += qr[i].x * kv.x + qr[i].y * kv.y + qr[i].z * kv.z + qr[i].w * kv.w;
+    }
+    const float sc = acc * scale;
+    score[j] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = block_max(mx, red);
+  float sum = 0.f;
+  for (uint32_t j = threadIdx.x; j <= t; j += blockDim.x) {
+    const float pj = expf(score[j] - mx);
+    score[j] = pj;
+    sum += pj;
+  }
+  const float l = block_sum(sum, red);
+  __syncthreads(); // every p_j is in LDS
+  const int qd = int(threadIdx.x) & 15, grp = int(threadIdx.x) >> 4;
+  const f4 *v4 = reinterpret_cast<const f4 *>(vh) + qd;
+  f4 acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t j0 = uint32_t(grp); j0 <= t; j0 += 128) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t j = j0 + 16u * u;
+      if (j <= t) acc[u] += score[j] * v4[size_t(j) * (HD / 4)];
+    }
+  }
+  f4 sum4 = acc[0];
+#pragma unroll
+  for (int u = 1; u < 8; ++u) sum4 += acc[u];
+  part[grp * 16 + qd] = sum4;
+  __syncthreads();
+  if (grp == 0) {
+    f4 r = part[qd];
+    for (int g2 = 1; g2 < 16; ++g2) r += part[g2 * 16 + qd];
+    reinterpret_cast<f4 *>(o + size_t(blockIdx.x) * HD)[qd] = r / l;
+  }
+}
+
 } // namespace
+
+TLH_API int tlh_attention_decode(const float *q, const float *k, const float *v, float *o,
+                                 uint32_t heads, uint32_t t_stride, uint32_t t,
+                                 uint32_t head_dim, float scale, void *stream) {
+  if (head_dim != HD || t >= t_stride || t_stride > kDecodeMaxT) return int(hipErrorInvalidValue);
+  if (heads == 0) return 0;
+  const size_t lds = (((t + 1 + 3) & ~3u) + 16 * 16 * 4 + 4) * sizeof(float);
+  attn_decode_kernel<<<heads, 256, lds, as_stream(stream)>>>(q, k, v, o, t_stride, t, scale);
+  return launch_status();
+}
 
 TLH_API int tlh_attention_forward(const float *q, const float *k, const float *v, float *o,
                                   float *lse, uint32_t batch, uint32_t heads, uint32_t seq,

@@ -884,8 +884,8 @@ TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
   if (d.M < 0 || d.N < 0 || d.K < 0) return int(hipErrorInvalidValue);
   if ((d.epilogue == tlh::kEpiGelu || d.epilogue == tlh::kEpiGeluBwd) && !d.aux)
     return int(hipErrorInvalidValue);
-  if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 || d.M % d.remap_t ||
-                        d.N != d.remap_h * d.remap_d))
+  if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 ||
+                        (d.M % d.remap_t && d.M > d.remap_t) || d.N != d.remap_h * d.remap_d))
     return int(hipErrorInvalidValue);
   if (desc->batch > 1 && (d.aux || d.epilogue != tlh::kEpiStore ||
                           (d.residual && !d.sum_batches)))

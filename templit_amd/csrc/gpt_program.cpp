@@ -315,6 +315,67 @@ int forward(Program &p, uint32_t seq) {
   return gemm(p, d);
 }
 
+// One position of the forward for incremental decoding (batch 1): the token
+// at position t (already in tokens[t]) through every block, extending and
+// reading the K/V planes that a forward over the window left (their T
+// stride is cfg.seq, so position t's keys and values land where the
+// window's forward put them). Row 0 of the activation buffers is scratch;
+// logits row 0 receives position t's logits. The same arithmetic as row t of
+// the window's forward: causal attention never lets row t see later rows.
+int decode_step(Program &p, uint32_t t) {
+  const tlg_config &c = p.cfg;
+  const int D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
+  TRY(tlh_embedding_add_positions(p.P(0), c.vocab, p.P(1) + size_t(t) * c.dim, p.tokens + t, 1,
+                                  1, c.dim, p.x[0], p.stream));
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    const uint32_t w = 2 + 12 * l;
+    TRY(tlh_rms_norm(p.x[l], nullptr, p.n1[l], nullptr, 1, c.dim, kRmsEps, p.stream));
+    {
+      // Q, K, V of position t, written into the planes at row t: the head
+      // remap of row 0 with a T stride of cfg.seq, offset by t rows.
+      tlh_gemm_desc d =
+          desc(p.n1[l], p.P(w), p.q[l] + size_t(t) * kHeadDim, 1, D, D, false, false);
+      d.bias = p.P(w + 1);
+      d.remap_t = int(c.seq);
+      d.remap_h = int(c.heads);
+      d.remap_d = int(kHeadDim);
+      d.batch = 3;
+      d.batch_stride_a = 0;
+      d.batch_stride_b = uint32_t(p.P(w + 2) - p.P(w));
+      d.batch_stride_c = uint32_t(p.k[l] - p.q[l]);
+      d.bias_batch_stride = uint32_t(p.P(w + 3) - p.P(w + 1));
+      TRY(gemm(p, d));
+    }
+    TRY(tlh_attention_decode(p.q[l], p.k[l], p.v[l], p.o[l], c.heads, c.seq, t, kHeadDim,
+                             1.0f / std::sqrt(float(kHeadDim)), p.stream));
+    {
+      tlh_gemm_desc d = desc(p.o[l], p.P(w + 6), p.x_mid[l], 1, D, D, false, false);
+      d.bias = p.P(w + 7);
+      d.residual = p.x[l];
+      TRY(gemm(p, d));
+    }
+    TRY(tlh_rms_norm(p.x_mid[l], nullptr, p.n2[l], nullptr, 1, c.dim, kRmsEps, p.stream));
+    {
+      tlh_gemm_desc d = desc(p.n2[l], p.P(w + 8), p.g[l], 1, F, D, false, false);
+      d.bias = p.P(w + 9);
+      d.epilogue = TLH_EPI_GELU;
+      d.aux = p.u[l];
+      TRY(gemm(p, d));
+    }
+    {
+      tlh_gemm_desc d = desc(p.g[l], p.P(w + 10), p.x[l + 1], 1, D, F, false, false);
+      d.bias = p.P(w + 11);
+      d.residual = p.x_mid[l];
+      TRY(gemm(p, d));
+    }
+  }
+  TRY(tlh_rms_norm(p.x[c.layers], nullptr, p.nf, nullptr, 1, c.dim, kRmsEps, p.stream));
+  const uint32_t last = 2 + 12 * c.layers;
+  tlh_gemm_desc d = desc(p.nf, p.P(last), p.logits, 1, V, D, false, false);
+  d.bias = p.P(last + 1);
+  return gemm(p, d);
+}
+
 // Input gradients run on the main stream; each weight gradient forks to the
 // side stream as soon as its upstream gradient exists, and the main stream
 // waits for it only before overwriting that gradient's buffer: dx is updated
@@ -529,6 +590,17 @@ int create(Program &p) {
   for (auto &s : linears) {
     uses.push_back(desc(nullptr, nullptr, nullptr, int(R), s[0], s[1], false, false));
     uses.push_back(desc(nullptr, nullptr, nullptr, int(R), s[1], s[0], false, true));
+  }
+  if (c.batch == 1) {
+    // decode_step: one row through every linear (split K: a single row
+    // gives only N/64 output tiles), Q/K/V batched
+    for (auto &s : linears) uses.push_back(desc(nullptr, nullptr, nullptr, 1, s[0], s[1], false, false));
+    tlh_gemm_desc d = desc(nullptr, nullptr, nullptr, 1, int(D), int(D), false, false);
+    d.batch = 3;
+    d.batch_stride_a = 0;
+    d.batch_stride_b = uint32_t(D * D + D);
+    d.batch_stride_c = uint32_t(R * D);
+    uses.push_back(d);
   }
   for (auto &d : uses) {
     size_t e = 0;
@@ -783,17 +855,41 @@ int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t pro
   std::vector<uint32_t> context(c.seq, eos_token);
   std::copy(host_prompt, host_prompt + prompt_len, context.begin());
   uint32_t valid = prompt_len;
+  // prefix_only == 2 (KV cache): after the first window forward, each new
+  // position runs through decode_step alone while the window has room.
+  bool cached = false;
+  auto next_token = [&](uint32_t &token) -> int {
+    TRY(tlh_memcpy_d2h(&token, p.argmax_out, sizeof(token), p.stream));
+    return tlh_stream_synchronize(p.stream);
+  };
   for (uint32_t g = 0; g < n_new; ++g) {
-    const uint32_t seq = prefix_only ? valid : c.seq;
+    if (cached) {
+      const uint32_t t = valid - 1; // the newest token's position
+      TRY(tlh_memcpy_h2d(p.tokens + t, &context[t], sizeof(uint32_t), p.stream));
+      TRY(decode_step(p, t));
+      TRY(tlh_argmax(p.logits, c.vocab, p.argmax_out, p.stream));
+      uint32_t token = 0;
+      TRY(next_token(token));
+      host_out[g] = token;
+      if (valid < c.seq) {
+        context[valid++] = token;
+      } else {
+        std::move(context.begin() + 1, context.end(), context.begin());
+        context.back() = token;
+        cached = false; // the window slid: every position moved
+      }
+      continue;
+    }
+    const uint32_t seq = prefix_only == 1 ? valid : c.seq;
     TRY(tlh_memcpy_h2d(p.tokens, context.data(), size_t(seq) * sizeof(uint32_t), p.stream));
     TRY(forward(p, seq));
     TRY(tlh_argmax(p.logits + size_t(valid - 1) * c.vocab, c.vocab, p.argmax_out, p.stream));
     uint32_t token = 0;
-    TRY(tlh_memcpy_d2h(&token, p.argmax_out, sizeof(token), p.stream));
-    TRY(tlh_stream_synchronize(p.stream));
+    TRY(next_token(token));
     host_out[g] = token;
     if (valid < c.seq) {
       context[valid++] = token;
+      cached = prefix_only == 2; // the window's K/V planes now serve decode_step
     } else {
       std::move(context.begin() + 1, context.end(), context.begin());
       context.back() = token;

@@ -132,6 +132,7 @@ HIP_SIGNATURES: dict[str, list] = {
     # attention
     "tlh_attention_forward": [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32,
                               c_float, c_int, c_int, P],
+    "tlh_attention_decode": [P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_float, P],
     "tlh_attention_backward": [P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                c_uint32, c_float, c_int, c_int, c_int, P],
     # optimiser
@@ -428,7 +429,9 @@ class GptProgram:
         check(self.lib.tlg_forward(self.handle), "forward")
 
     def generate_greedy(self, prompt, n_new, eos_token, prefix_only=False):
-        """Greedy tokens after `prompt` (inference::autoregression, top_k 1)."""
+        """Greedy tokens after `prompt` (inference::autoregression, top_k 1).
+        prefix_only: False / 0 recomputes the padded window per token, True / 1
+        the valid prefix, 2 keeps a KV cache (tlg_generate_greedy)."""
         pr = self._np.ascontiguousarray(prompt, dtype=self._np.uint32)
         out = self._np.empty(n_new, self._np.uint32)
         check(self.lib.tlg_generate_greedy(self.handle, pr.ctypes.data, pr.size, n_new, eos_token,

@@ -358,7 +358,7 @@ def _greedy_reference_check(cfg, params, prompt, generated, eos):
     return exact
 
 
-@pytest.mark.parametrize("prefix_only", [False, True])
+@pytest.mark.parametrize("prefix_only", [False, True, 2])  # 2: KV cache
 def test_greedy_generation_matches_oracle(prefix_only):
     V, T, D, H, L = 96, 32, 128, 2, 2
     cfg = O.gpt_config(V, T, D, H, L, 1)
@@ -390,3 +390,24 @@ def test_greedy_prefix_equals_full_window():
     finally:
         prog.close()
     np.testing.assert_array_equal(full, pref)
+
+
+def test_greedy_kv_cache_equals_full_window():
+    # The KV cache computes each new position alone (decode attention over
+    # the cached keys) until the window is full, then recomputes: 9 + 60
+    # tokens slide past T = 48, so both phases are covered.
+    V, T, D, H, L = 64, 48, 128, 2, 2
+    cfg = O.gpt_config(V, T, D, H, L, 1)
+    total = int(sum(O.gpt_param_sizes(cfg)))
+    params = O.normal((total,), 710, 0, 0.2)
+    prompt = O.uniform_u32((9,), 711, V)
+    prog = GptProgram(V, T, D, H, L, 1)
+    try:
+        prog.set_params(params)
+        full = prog.generate_greedy(prompt, 60, 0, prefix_only=False)
+        kv = prog.generate_greedy(prompt, 60, 0, prefix_only=2)
+        again = prog.generate_greedy(prompt, 60, 0, prefix_only=2)
+    finally:
+        prog.close()
+    np.testing.assert_array_equal(full, kv)
+    np.testing.assert_array_equal(kv, again)

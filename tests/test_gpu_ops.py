@@ -753,6 +753,25 @@ def test_adamw_multi_matches_per_tensor(g):
         assert_close(g.host(dev[3][i]), em2, rtol=1e-4, atol=1e-9, what=f"m2 {i}")
 
 
+@pytest.mark.parametrize("H,stride,t", [(2, 64, 0), (4, 1024, 1), (3, 100, 57), (16, 1024, 255),
+                                        (16, 1024, 1023)])
+def test_attention_decode(g, H, stride, t):
+    # One query at position t over keys 0..t of [H, stride, 64] planes equals
+    # row t of causal attention over the first t + 1 positions.
+    q, k, v = (O.normal((1, H, stride, 64), s, 0, 0.125) for s in (130, 131, 132))
+    o_ref, _ = O.attention_forward(q[:, :, :t + 1], k[:, :, :t + 1], v[:, :, :t + 1], True)
+    o = g.empty((H * 64,))
+    g.call("tlh_attention_decode", g.dev(q), g.dev(k), g.dev(v), o, H, stride, t, 64, 0.125)
+    assert_rel(g.host(o).reshape(H, 64), o_ref[0, :, t, :], 1e-3, "decode O")
+
+
+def test_attention_decode_rejects_bad_positions(g):
+    q = g.empty((2 * 16 * 64,))
+    for stride, t, hd in ((16, 16, 64), (16, 3, 32), (9000, 5, 64)):
+        assert g.lib.tlh_attention_decode(q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), 2,
+                                          stride, t, hd, 0.125, g.stream) != 0
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------
