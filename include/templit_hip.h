@@ -244,7 +244,10 @@ typedef struct tlh_gemm_desc {
 } tlh_gemm_desc;
 
 int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
-/* fp32 elements of workspace tlh_gemm wants for `desc` (0: none needed). */
+/* fp32 elements of workspace tlh_gemm wants for `desc` (0: none needed).
+ * One-row products (m = 1, neither operand transposed, b float4-aligned, no
+ * bias gradient) run as a GEMV over K chunks when a workspace is given:
+ * their chunk sums are added in a fixed order (deterministic). */
 int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
 /* Tuning hook: force every following tlh_gemm / tlh_matmul to use a
  * bm x bn tile (64 or 128 each), a K tile of bk (16 or 32) and, where a
@@ -253,8 +256,9 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * count needs a workspace sized for it (tlh_gemm_workspace_size).
  * bk = -1 / -2 instead switches the XCD-aware block order off / on
  * (default on), bk = -3 / -4 the tail split off / on (default on),
- * bk = -5 / -6 the rectangular XCD tile blocks off / on (default on); these
- * leave the plan alone. */
+ * bk = -5 / -6 the rectangular XCD tile blocks off / on (default on),
+ * bk = -7 / -8 the one-row (GEMV) path off / on (default on); these leave
+ * the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

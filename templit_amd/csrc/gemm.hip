@@ -439,6 +439,72 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   store_acc<BN, TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
 }
 
+// ---- one-row products (M = 1): GEMV ------------------------------------------
+// y = x . B with x [1, K] and B [K, N] row-major: memory-bound on B, and a
+// 64-row MFMA tile would compute 63 rows of padding. Pass 1: block (256
+// output columns x, K chunk y, entry z) -- the 64 lanes across the columns
+// in float4, the 4 waves over the chunk's rows, 4 loads in flight per lane --
+// writes its column sums to partials[entry][chunk][N]. Pass 2 adds the
+// chunks in a fixed order and applies the epilogue (deterministic).
+__global__ __launch_bounds__(256) void gemv_partial_kernel(GemmParams p, int chunk_k,
+                                                           int chunks) {
+  __shared__ f4 part[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c4 = int(blockIdx.x) * 64 + lane; // float4 column
+  const int entry = int(blockIdx.z);
+  const float *A = p.A + (p.batch_ndim > 0 ? size_t(entry) * p.bsa[0] : 0);
+  const f4 *B4 = reinterpret_cast<const f4 *>(p.B + (p.batch_ndim > 0 ? size_t(entry) * p.bsb[0] : 0));
+  const size_t ldb4 = size_t(p.ldb) / 4;
+  const int k0 = int(blockIdx.y) * chunk_k;
+  const int k1 = min(p.K, k0 + chunk_k);
+  f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0, a3 = a0;
+  if (c4 * 4 < p.N) {
+    int k = k0 + w;
+    for (; k + 12 < k1; k += 16) {
+      a0 += A[k] * B4[size_t(k) * ldb4 + c4];
+      a1 += A[k + 4] * B4[size_t(k + 4) * ldb4 + c4];
+      a2 += A[k + 8] * B4[size_t(k + 8) * ldb4 + c4];
+      a3 += A[k + 12] * B4[size_t(k + 12) * ldb4 + c4];
+    }
+    for (; k < k1; k += 4) a0 += A[k] * B4[size_t(k) * ldb4 + c4];
+  }
+  part[w][lane] = (a0 + a1) + (a2 + a3);
+  __syncthreads();
+  if (w == 0 && c4 * 4 < p.N) {
+    const f4 t = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    reinterpret_cast<f4 *>(p.workspace)[(size_t(entry) * chunks + blockIdx.y) * (p.N / 4) + c4] = t;
+  }
+}
+
+// Pass 2: block (64 columns x, entry y); wave w adds chunks w, w + 4, ...
+// (8 loads in flight, coalesced across the lanes' columns); the 4 wave sums
+// are added in wave order.
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(GemmParams p, int chunks) {
+  __shared__ float wsum[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = int(blockIdx.x) * 64 + lane, entry = int(blockIdx.y);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (n < p.N) {
+    const float *part = p.workspace + size_t(entry) * chunks * p.N + n;
+    for (int c0 = w; c0 < chunks; c0 += 32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c0 + 4 * j < chunks) acc[j] += part[size_t(c0 + 4 * j) * p.N];
+    }
+  }
+  float v = acc[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) v += acc[j];
+  wsum[w][lane] = v;
+  __syncthreads();
+  if (w == 0 && n < p.N) {
+    const float t = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+    float *C = p.C + (p.batch_ndim > 0 ? size_t(entry) * p.bsc[0] : 0);
+    const float *bias = p.bias ? p.bias + size_t(entry) * p.bias_bstride : nullptr;
+    epilogue_store(p, bias, C, 0, n, t);
+  }
+}
+
 // Sums the split-K partials of every output entry in split order --
 // deterministic -- and applies the epilogue.
 // VEC4: the plane is read as float4 (N % 4 == 0, so the 4 elements of a
@@ -557,6 +623,7 @@ constexpr int kTargetBlocks = 256; // one block per CU at least
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
 int g_xcd_remap = 1;
 int g_xcd_rects = 1;
+int g_gemv = 1;
 
 // The 8-way partition of a tiles_m x tiles_n grid into equal rectangles
 // (1x8, 2x4, 4x2 or 8x1 of them) whose rectangle needs the fewest operand
@@ -642,6 +709,32 @@ bool vec_ok(const GemmDesc &d) {
   return true;
 }
 
+// One-row products that take the GEMV path: x [1, K], B [K, N] row-major
+// and float4-aligned, one batch dimension at most, no bias gradient.
+bool gemv_ok(const GemmDesc &d) {
+  if (d.M != 1 || d.trans_a || d.trans_b || d.bias_grad || d.sum_batches || d.K < 64) return false;
+  if (d.batch_ndim > 1 || (d.batch_ndim == 0 && d.batch > 1)) return false;
+  if (d.N % 4 || d.ldb % 4 || (reinterpret_cast<uintptr_t>(d.B) & 15)) return false;
+  return d.batch_ndim == 0 || d.batch_stride_b[0] % 4 == 0;
+}
+
+// K chunks of the GEMV: about 256 blocks, chunks of >= 64 rows (multiples
+// of 16: 4 waves x 4 loads in flight).
+struct GemvPlan {
+  int chunks = 1, chunk_k = 0;
+};
+GemvPlan gemv_plan(const GemmDesc &d) {
+  GemvPlan g;
+  const long col_blocks = (d.N + 255) / 256, entries = std::max(1, d.batch);
+  long chunks = std::max<long>(1, 256 / (col_blocks * entries));
+  chunks = std::min<long>(chunks, std::max(1, d.K / 64));
+  long ck = (d.K + chunks - 1) / chunks;
+  ck = (ck + 15) / 16 * 16;
+  g.chunk_k = int(ck);
+  g.chunks = int((d.K + ck - 1) / ck);
+  return g;
+}
+
 } // namespace
 
 int gemm_choose_splits(const GemmDesc &d) { return make_plan(d, true).splits; }
@@ -698,6 +791,7 @@ TailSplit tail_split(const GemmDesc &d, const Plan &plan, int K) {
 int folded_k(const GemmDesc &d) { return d.sum_batches ? d.K * d.batch : d.K; }
 
 size_t gemm_workspace_elems(const GemmDesc &d) {
+  if (gemv_ok(d)) return size_t(std::max(1, d.batch)) * gemv_plan(d).chunks * size_t(d.N);
   const Plan plan = make_plan(d, true);
   const int s = plan.splits;
   const size_t outputs = d.sum_batches ? 1 : size_t(std::max(1, d.batch));
@@ -744,6 +838,16 @@ int gemm_launch(const GemmDesc &d, void *stream) {
     p.bsa[i] = d.batch_stride_a[i];
     p.bsb[i] = d.batch_stride_b[i];
     p.bsc[i] = d.batch_stride_c[i];
+  }
+  if (gemv_ok(d) && d.workspace && g_gemv &&
+      (!d.workspace_elems || gemm_workspace_elems(d) <= d.workspace_elems)) {
+    const GemvPlan gp = gemv_plan(d);
+    dim3 grid(unsigned((d.N + 255) / 256), unsigned(gp.chunks), unsigned(p.batch));
+    gemv_partial_kernel<<<grid, 256, 0, s>>>(p, gp.chunk_k, gp.chunks);
+    if (const int st = launch_status()) return st;
+    gemv_reduce_kernel<<<dim3(unsigned((d.N + 63) / 64), unsigned(p.batch)), 256, 0, s>>>(
+        p, gp.chunks);
+    return launch_status();
   }
   Plan plan = make_plan(d, d.workspace != nullptr);
   if (plan.splits > 1 && d.workspace_elems && gemm_workspace_elems(d) > d.workspace_elems)
@@ -867,6 +971,10 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   }
   if (bk == -5 || bk == -6) {
     tlh::g_xcd_rects = bk == -6;
+    return 0;
+  }
+  if (bk == -7 || bk == -8) {
+    tlh::g_gemv = bk == -8;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));

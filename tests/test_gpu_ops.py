@@ -231,6 +231,38 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, 16), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -4), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -6), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -8), "set_plan")
+
+
+@pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
+                                 (64, 4)])
+@pytest.mark.parametrize("variant", ["plain", "bias_residual", "gelu", "beta"])
+def test_gemm_one_row(g, forced_plan, K, N, variant):
+    # m = 1 with a workspace runs the GEMV path (K chunks summed in a fixed
+    # order); it matches the oracle and the MFMA tile path.
+    a, b = O.normal((1, K), 50, 0, 0.5), O.normal((K, N), 51, 0, 0.5)
+    ref = O.matmul(a, b)
+    kw = {}
+    if variant == "bias_residual":
+        bias, res = O.normal((N,), 52), O.normal((1, N), 53)
+        kw = dict(bias=bias, residual=res)
+        ref = O.binary("add", O.binary("add", ref, bias.reshape(1, -1)), res)
+    elif variant == "gelu":
+        bias = O.normal((N,), 54)
+        kw = dict(bias=bias, epi=EPI_GELU)
+        pre = O.binary("add", ref, bias.reshape(1, -1))
+        ref = O.unary("gelu", pre)
+    elif variant == "beta":
+        c0 = O.normal((1, N), 55)
+        kw = dict(beta=0.5, c_init=c0)
+        ref = ref + np.float32(0.5) * c0
+    out, aux = gemm(g, a, b, **kw)
+    assert_rel(out.reshape(1, N), ref, 1e-3, "gemv")
+    if variant == "gelu":
+        assert_rel(aux.reshape(1, N), pre, 1e-3, "gemv pre-activation")
+    forced_plan(0, 0, 0, -7)  # the MFMA tile path
+    out_tiles, _ = gemm(g, a, b, **kw)
+    assert_rel(out.reshape(1, N), out_tiles.reshape(1, N), 1e-4, "gemv vs tiles")
 
 
 @pytest.mark.parametrize("M,N,K,ta", [(384, 2048, 6144, True), (384, 1536, 6144, True),
