@@ -276,14 +276,20 @@ __global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__res
   const float *src = a + size_t(z) * in_batch_stride;
   float *dst = out + size_t(z) * rows * cols;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const uint32_t in_row = j0 + r, in_col = i0 + tx;
-    if (in_row < cols && in_col < rows) tile[r][tx] = src[size_t(in_row) * ld_in + in_col];
+  // all 16 loads of a thread in flight before the LDS writes
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t in_row = j0 + ty + 4 * i, in_col = i0 + tx;
+    v[i] = (in_row < cols && in_col < rows) ? src[size_t(in_row) * ld_in + in_col] : 0.f;
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tile[ty + 4 * i][tx] = v[i];
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const uint32_t o_row = i0 + r, o_col = j0 + tx;
-    if (o_row < rows && o_col < cols) dst[size_t(o_row) * cols + o_col] = tile[tx][r];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t o_row = i0 + ty + 4 * i, o_col = j0 + tx;
+    if (o_row < rows && o_col < cols) dst[size_t(o_row) * cols + o_col] = tile[tx][ty + 4 * i];
   }
 }
 
