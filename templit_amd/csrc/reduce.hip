@@ -126,24 +126,33 @@ __global__ __launch_bounds__(256) void col_partials_kernel(const float *__restri
   }
 }
 
-// Pass 2 keeps 8 chunk loads in flight per column: accumulator j takes
-// chunks j, j + 8, ..., and the accumulators are added in j order.
-__global__ __launch_bounds__(64) void col_finish_kernel(const float *__restrict__ partials,
-                                                        float *__restrict__ out, uint32_t chunks,
-                                                        uint32_t cols, float beta) {
-  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
+// Pass 2: block per 64 columns; wave w adds chunks w, w + 4, ... (8 loads
+// in flight, coalesced across the lanes' columns), and the 4 wave sums are
+// added in wave order.
+__global__ __launch_bounds__(256) void col_finish_kernel(const float *__restrict__ partials,
+                                                         float *__restrict__ out, uint32_t chunks,
+                                                         uint32_t cols, float beta) {
+  __shared__ float wsum[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t c = blockIdx.x * 64 + uint32_t(lane);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (uint32_t k0 = 0; k0 < chunks; k0 += 8) {
+  if (c < cols) {
+    for (uint32_t k0 = uint32_t(w); k0 < chunks; k0 += 32) {
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j)
-      if (k0 + j < chunks) acc[j] += partials[size_t(k0 + j) * cols + c];
+      for (uint32_t j = 0; j < 8; ++j)
+        if (k0 + 4 * j < chunks) acc[j] += partials[size_t(k0 + 4 * j) * cols + c];
+    }
   }
   float t = acc[0];
 #pragma unroll
   for (int j = 1; j < 8; ++j) t += acc[j];
-  if (beta != 0.0f) t += beta * out[c];
-  out[c] = t;
+  wsum[w][lane] = t;
+  __syncthreads();
+  if (w == 0 && c < cols) {
+    float r = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+    if (beta != 0.0f) r += beta * out[c];
+    out[c] = r;
+  }
 }
 
 // Row chunking of the two-pass column sum: about 512 blocks, chunks of at
@@ -275,8 +284,8 @@ int reduce_to_shape(const float *a, float *out, uint32_t ndim, const uint32_t *a
       col_partials_kernel<<<dim3(ceil_div(shp[1], 64), cs.chunks), 256, 0, s>>>(
           a, workspace, shp[0], shp[1], cs.chunk_rows);
       if (const int st = launch_status()) return st;
-      col_finish_kernel<<<ceil_div(shp[1], 64), 64, 0, s>>>(workspace, out, cs.chunks, shp[1],
-                                                             0.0f);
+      col_finish_kernel<<<ceil_div(shp[1], 64), 256, 0, s>>>(workspace, out, cs.chunks, shp[1],
+                                                              0.0f);
       return launch_status();
     }
     col_reduce_kernel<MAX><<<ceil_div(shp[1], 32), 256, 0, s>>>(a, out, shp[0], shp[1], 0.0f);
