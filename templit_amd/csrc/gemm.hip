@@ -661,10 +661,15 @@ constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 //  - 128x128 tiles (K tile 16) only when they give every CU three or more
 //    blocks and pad the output little more than 64x64 tiles do (192x192
 //    attention scores: 4 tiles of 128 cover 1.8x the area, 9 of 64 exactly,
-//    and run 2x faster); their 4 accumulators per wave win when the grid is
+//    and run 2x faster) and K >= 384 (with K = 192 the tile's fill and
+//    epilogue outweigh its reuse: the reference executor's per-sequence
+//    weight gradients [32 x 384x192 . 192x1536] take 118 us on 128x128 tiles,
+//    90 us on 64x64); their 4 accumulators per wave win when the grid is
 //    deep;
-//  - otherwise 64x64 tiles with a K tile of 32: 2-4 co-resident blocks per
-//    CU hide the global/LDS latency a single block per CU cannot;
+//  - otherwise 64x64 tiles with a K tile of 32 (16 when K <= 256: the
+//    executor's K = 64 attention scores 19 us instead of 23): 2-4
+//    co-resident blocks per CU hide the global/LDS latency a single block
+//    per CU cannot;
 //  - tall-K products (weight gradients, K = B*T) with too few output tiles
 //    split K so that about 768 blocks (3 per CU) run, each with K chunks of
 //    >= 256 ([384,2048] with K = 6144: 4 splits, 10% faster than 8).
@@ -682,7 +687,7 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
     return double(d.M) * double(d.N) /
            (double((d.M + bm - 1) / bm * bm) * double((d.N + bn - 1) / bn * bn));
   };
-  if (tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
+  if (K >= 384 && tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
       coverage(128, 128) >= 0.9 * coverage(64, 64))
     return {128, 128, 1, 16};
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
@@ -693,7 +698,7 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
       splits *= 2;
     if (splits >= 2) return {64, 64, splits, 32};
   }
-  return {64, 64, 1, 32};
+  return {64, 64, 1, K <= 256 ? 16 : 32};
 }
 
 bool vec_ok(const GemmDesc &d) {
