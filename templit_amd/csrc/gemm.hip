@@ -670,6 +670,9 @@ constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 //    executor's K = 64 attention scores 19 us instead of 23): 2-4
 //    co-resident blocks per CU hide the global/LDS latency a single block
 //    per CU cannot;
+//  - K >= 1024 with at least 3 tiles of 64x128 per CU: 64x128 tiles (K tile
+//    16), also in place of 128x128 when B is transposed (the d = 1024 / T =
+//    1024 shapes: 4-7% faster than 64x64, and than 128x128 for dG);
 //  - tall-K products (weight gradients, K = B*T) with too few output tiles
 //    split K so that about 768 blocks (3 per CU) run, each with K chunks of
 //    >= 256 ([384,2048] with K = 6144: 4 splits, 10% faster than 8).
@@ -689,9 +692,16 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   };
   if (K >= 384 && tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
       coverage(128, 128) >= 0.9 * coverage(64, 64))
-    return {128, 128, 1, 16};
+    return (K >= 1024 && d.trans_b) ? Plan{64, 128, 1, 16} : Plan{128, 128, 1, 16};
+  if (K >= 1024 && tiles_for(d, 64, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
+      coverage(64, 128) >= 0.9 * coverage(64, 64))
+    return {64, 128, 1, 16};
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
-  if (allow_split && one_dim && tiles < size_t(kTargetBlocks) && K >= 2 * kMinSplitK) {
+  // weight gradients (transposed A, K = tokens) split K below 3 tiles per CU:
+  // one long whole-K block per CU runs [1024,1024] x K 8192 at 72 TFLOP/s, 8
+  // splits at 105
+  const size_t split_below = (d.trans_a ? 3 : 1) * size_t(kTargetBlocks);
+  if (allow_split && one_dim && tiles < split_below && K >= 2 * kMinSplitK) {
     int splits = 1;
     while (splits < 16 && tiles * size_t(splits) < 3 * size_t(kTargetBlocks) &&
            K / (splits * 2) >= kMinSplitK)
