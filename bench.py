@@ -252,8 +252,9 @@ def time_steps(prog, step, warmup: int, steps: int) -> float:
 
 def scaled_gpt(steps: int, gen_tokens: int) -> dict:
     """The scaled configuration: d 1024, 16 heads, 12 blocks, T 1024, V 2048,
-    batch 8 -- a training step (eager launches on the program's two streams;
-    the hipGraph replay of the same step is timed too) and greedy generation of
+    batch 8 -- a training step (eager launches on the streams the program
+    picks for this size; the hipGraph replay of the same step and the other
+    stream choice are timed too) and greedy generation of
     `gen_tokens` tokens from a 32-token random prompt (batch 1: the reference's
     full-window recompute, the equivalent valid-prefix recompute, and a KV
     cache that runs each new position alone)."""
@@ -269,17 +270,24 @@ def scaled_gpt(steps: int, gen_tokens: int) -> dict:
         prog.set_optimizer(**HP)
         prog.random_batch(seed=22)
         eager = lambda: prog.train_step(1.0 / tokens, MAX_NORM)
+        streams = lambda two: "two streams" if two else "one stream"
+        two = prog.set_concurrency(-1)
         dt = time_steps(prog, eager, 2, steps)
         model_flops = 6.0 * prog.total * tokens  # excludes attention's T^2 term
         out["train"] = {"tokens_per_step": tokens, "ms_per_step": round(dt * 1e3, 3),
                         "tokens_per_s": round(tokens / dt, 1), "steps": steps,
-                        "execution": "eager launches on two streams",
+                        "execution": f"eager launches on {streams(two)}",
                         "loss": round(float(prog.losses().mean()), 4),
                         "param_flops_tflops": round(model_flops / dt / 1e12, 2)}
         prog.capture(1.0 / tokens, MAX_NORM)
         dt = time_steps(prog, prog.replay, 2, steps)
         out["train_graph_replay"] = {"ms_per_step": round(dt * 1e3, 3),
                                      "tokens_per_s": round(tokens / dt, 1)}
+        prog.set_concurrency(int(not two))
+        dt = time_steps(prog, eager, 2, steps)
+        out["train_other_streams"] = {"execution": f"eager launches on {streams(not two)}",
+                                      "ms_per_step": round(dt * 1e3, 3),
+                                      "tokens_per_s": round(tokens / dt, 1)}
     finally:
         prog.close()
     log(f"[bench] scaled train: {out['train']}")

@@ -70,6 +70,16 @@ int tlg_set_optimizer(void *program, float lr, float beta1, float beta2, float e
                       float weight_decay);
 int tlg_set_lr(void *program, float lr);
 
+/* Streams of the training step: 1 runs the weight gradients on a second
+ * stream beside the chain of input gradients (fork/join events order
+ * them), 0 runs the whole step on the program's stream, -1 (the default at
+ * tlg_create) picks 1 while the [batch*seq, dim] products have fewer than
+ * 4 tiles of 64x64 per compute unit and 0 above. Results are bitwise the
+ * same either way (every kernel is deterministic). Applies to steps issued
+ * or captured after the call. tlg_get_concurrency reports the choice. */
+int tlg_set_concurrency(void *program, int mode);
+int tlg_get_concurrency(void *program, int *two_streams);
+
 /* Device buffers the step reads its batch from (uint32 [B*T] each) and
  * writes per-row losses to (float [B*T]); stable for the program's life. */
 int tlg_io(void *program, uint32_t **tokens, uint32_t **targets, float **losses,

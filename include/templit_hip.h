@@ -45,6 +45,8 @@ extern "C" {
  * idempotent for the same device. */
 int tlh_init(int device);
 int tlh_device_count(int *count);
+/* Compute units of the current device (256 on MI355X). */
+int tlh_device_cu_count(int *count);
 const char *tlh_error_string(int code);
 int tlh_device_synchronize(void);
 

@@ -90,6 +90,13 @@ TLH_API int tlh_init(int device) {
 
 TLH_API int tlh_device_count(int *count) { return int(hipGetDeviceCount(count)); }
 
+TLH_API int tlh_device_cu_count(int *count) {
+  int device = 0;
+  const hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return int(st);
+  return int(hipDeviceGetAttribute(count, hipDeviceAttributeMultiprocessorCount, device));
+}
+
 TLH_API const char *tlh_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }

@@ -48,6 +48,7 @@ EPI_STORE, EPI_GELU, EPI_GELU_BWD = 0, 1, 2
 HIP_SIGNATURES: dict[str, list] = {
     "tlh_init": [c_int],
     "tlh_device_count": [POINTER(c_int)],
+    "tlh_device_cu_count": [POINTER(c_int)],
     "tlh_device_synchronize": [],
     "tlh_stream_create": [POINTER(c_void_p)],
     "tlh_stream_destroy": [P],
@@ -215,6 +216,8 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_init_params": [P, c_uint64, c_float],
     "tlg_set_optimizer": [P, c_float, c_float, c_float, c_float, c_float],
     "tlg_set_lr": [P, c_float],
+    "tlg_set_concurrency": [P, c_int],
+    "tlg_get_concurrency": [P, POINTER(c_int)],
     "tlg_io": [P, FP, FP, FP, FP],
     "tlg_train_step": [P, c_float, c_float, c_int],
     "tlg_forward": [P],
@@ -421,6 +424,14 @@ class GptProgram:
     def set_optimizer(self, lr, beta1, beta2, eps, weight_decay):
         check(self.lib.tlg_set_optimizer(self.handle, lr, beta1, beta2, eps, weight_decay),
               "tlg_set_optimizer")
+
+    def set_concurrency(self, mode):
+        """-1 automatic (the default), 0 one stream, 1 weight gradients on a
+        second stream; returns whether the step now uses two streams."""
+        check(self.lib.tlg_set_concurrency(self.handle, int(mode)), "tlg_set_concurrency")
+        out = c_int()
+        check(self.lib.tlg_get_concurrency(self.handle, ctypes.byref(out)), "tlg_get_concurrency")
+        return bool(out.value)
 
     def train_step(self, root_grad, max_norm, update=True):
         check(self.lib.tlg_train_step(self.handle, root_grad, max_norm, int(update)), "train_step")

@@ -173,6 +173,36 @@ def test_c4_concurrent_weight_gradients_match_serial(c4):
         assert np.array_equal(got, want), what
 
 
+def test_stream_choice_follows_the_tile_count():
+    # rows 6144 x dim 384 (576 tiles of 64x64 on 256 CUs) keeps the second
+    # stream; rows 4096 x dim 1024 (1024 tiles) runs on one stream, and
+    # forcing either choice changes no bit of the step
+    c4_shape = GptProgram(256, 192, 384, 6, 1, 32)
+    try:
+        assert c4_shape.set_concurrency(-1)
+    finally:
+        c4_shape.close()
+    prog = GptProgram(256, 512, 1024, 16, 1, 8)
+    try:
+        assert not prog.set_concurrency(-1)
+        runs = []
+        for mode in (0, 1):
+            assert prog.set_concurrency(mode) == bool(mode)
+            prog.init_params(seed=2, std=0.02)
+            prog.set_optimizer(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+            prog.random_batch(seed=9)
+            for _ in range(2):
+                prog.train_step(1.0 / 4096, 1.0)
+            prog.synchronize()
+            runs.append((prog.losses(), prog.get_grads(), prog.get_params()))
+        for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
+            assert np.array_equal(got, want), what
+        with pytest.raises(NativeError):
+            prog.set_concurrency(2)
+    finally:
+        prog.close()
+
+
 def read_archive(path):
     """name -> bytes of a checkpoint archive file (u32 name length, name,
     u32 blob length, blob)*."""
