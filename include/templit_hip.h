@@ -259,7 +259,9 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * bk = -1 / -2 instead switches the XCD-aware block order off / on
  * (default on), bk = -3 / -4 the tail split off / on (default on),
  * bk = -5 / -6 the rectangular XCD tile blocks off / on (default on),
- * bk = -7 / -8 the one-row (GEMV) path off / on (default on); these leave
+ * bk = -7 / -8 the one-row (GEMV) path off / on (default on), bk = -9 /
+ * -10 the float4 split-K reduce over a (plane, entry) grid off / on
+ * (default on; off runs the grid-stride reduce, same bits); these leave
  * the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 

@@ -562,6 +562,62 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams p) {
   }
 }
 
+// The float4 form of gemm_splitk_reduce<true> (N % 4 == 0, 16-byte aligned
+// planes, at most kMaxSplits splits): grid (float4 groups of one plane / 256,
+// entries); a thread issues the loads of all of its group's partials before
+// the adds, which keep gemm_splitk_reduce's order (even splits, odd splits,
+// then the two sums), so both kernels give the same bits. Thread i < N of
+// each entry also sums bias-gradient column i's partials.
+constexpr int kMaxSplits = 16;
+__global__ __launch_bounds__(256) void gemm_splitk_reduce4(GemmParams p) {
+  const size_t plane = size_t(p.M) * p.N;
+  const size_t plane4 = plane / 4;
+  const int b = blockIdx.y;
+  const int splits = p.splits;
+  float *C = p.C;
+  const float *bias = p.bias;
+  if (p.batch_ndim > 0) {
+    C += size_t(b) * p.bsc[0];
+    if (bias) bias += size_t(b) * p.bias_bstride;
+  }
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < plane4) {
+    const f4 *w = reinterpret_cast<const f4 *>(p.workspace + size_t(b) * splits * plane) + i;
+    f4 v[kMaxSplits];
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < splits) v[z] = w[size_t(z) * plane4];
+    f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int z = 0; z + 1 < kMaxSplits; z += 2) {
+      if (z + 1 < splits) {
+        s0 += v[z];
+        s1 += v[z + 1];
+      } else if (z < splits) {
+        s0 += v[z];
+      }
+    }
+    const f4 sum = s0 + s1;
+    const int m = int((i * 4) / p.N);
+    const int n = int(i * 4 - size_t(m) * p.N);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) epilogue_store(p, bias, C, m, n + e, sum[e]);
+  }
+  if (p.bias_grad && i < size_t(p.N)) {
+    float *bg = p.bias_grad + (p.batch_ndim > 0 ? size_t(b) * p.bias_bstride : 0);
+    const float *wb = p.workspace + size_t(p.batch) * splits * plane + size_t(b) * splits * p.N + i;
+    float v[kMaxSplits];
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < splits) v[z] = wb[z * size_t(p.N)];
+    float s = 0.f;
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < splits) s += v[z];
+    bg[i] = p.beta != 0.0f ? s + p.beta * bg[i] : s;
+  }
+}
+
 // Sums the tail tiles' K-chunk partials in chunk order -- deterministic --
 // and applies the epilogue. Float4 groups of a BM x BN tile (BN % 4 == 0).
 template <int BM, int BN>
@@ -574,8 +630,15 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce(GemmParams p) {
     const int t = int(g / (TILE / 4));
     const int e = int(g - size_t(t) * (TILE / 4)) * 4;
     const f4 *w = reinterpret_cast<const f4 *>(p.workspace + size_t(t) * p.tail_splits * TILE + e);
-    f4 sum = w[0];
-    for (int s = 1; s < p.tail_splits; ++s) sum += w[size_t(s) * (TILE / 4)];
+    // every chunk's load is issued before the adds (at most 16 chunks)
+    f4 v[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s)
+      if (s < p.tail_splits) v[s] = w[size_t(s) * (TILE / 4)];
+    f4 sum = v[0];
+#pragma unroll
+    for (int s = 1; s < kMaxSplits; ++s)
+      if (s < p.tail_splits) sum += v[s];
     const int tile = p.dp_tiles + t;
     const int tm = tile / p.tiles_n;
     const int m = tm * BM + e / BN;
@@ -624,6 +687,8 @@ int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
 int g_xcd_remap = 1;
 int g_xcd_rects = 1;
 int g_gemv = 1;
+// float4 split-K reduce over a (plane, entry) grid (see gemm_splitk_reduce4)
+int g_reduce4 = 1;
 
 // The 8-way partition of a tiles_m x tiles_n grid into equal rectangles
 // (1x8, 2x4, 4x2 or 8x1 of them) whose rectangle needs the fewest operand
@@ -928,7 +993,11 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   if (p.splits > 1) {
     // The workspace planes start 16-byte aligned when M*N is a multiple of 4.
     const bool v4 = d.N % 4 == 0 && (reinterpret_cast<uintptr_t>(d.workspace) & 15) == 0;
-    if (v4)
+    if (v4 && p.splits <= kMaxSplits && p.batch <= 65535 && g_reduce4)
+      gemm_splitk_reduce4<<<dim3(unsigned((std::max(reduce_elems / 4, size_t(d.N)) + 255) / 256),
+                                 unsigned(p.batch)),
+                            256, 0, s>>>(p);
+    else if (v4)
       gemm_splitk_reduce<true><<<stride_grid(reduce_elems / 4 + 1, 256), 256, 0, s>>>(p);
     else
       gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
@@ -990,6 +1059,10 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   }
   if (bk == -7 || bk == -8) {
     tlh::g_gemv = bk == -8;
+    return 0;
+  }
+  if (bk == -9 || bk == -10) {
+    tlh::g_reduce4 = bk == -10;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));

@@ -232,6 +232,7 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -4), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -6), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -8), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -10), "set_plan")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
@@ -409,6 +410,43 @@ def test_gemm_batched_weight_grads_with_bias_grads(g, K):
         bg = got[j * gap + M * N:j * gap + M * N + N]
         assert_rel(w, O.matmul(x.T, dys[j]), 1e-3, f"dW[{j}]")
         assert_close(bg, O.sum_to_shape(dys[j], [N]), rtol=1e-4, atol=1e-3, what=f"db[{j}]")
+
+
+@pytest.mark.parametrize("splits", [3, 8, 16])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+@pytest.mark.parametrize("M", [384, 2])
+def test_gemm_split_k_reducers_agree(g, forced_plan, splits, beta, M):
+    # The split-K partials are summed by a float4 kernel over a (plane,
+    # entry) grid or by the grid-stride kernel; both add in the same fixed
+    # order, so the weights and bias gradients agree bit for bit. M = 2:
+    # fewer float4 groups in a plane than bias-gradient columns.
+    N, K = 256, 6144
+    x = O.normal((K, M), 147, 0, 0.5)
+    dys = O.normal((3, K, N), 148, 0, 0.5)
+    gap = M * N + N + 64
+    init = O.normal((3 * gap,), 149, 0, 0.1)
+    outs = []
+    for toggle in (-9, -10):
+        forced_plan(0, 0, 0, toggle)
+        forced_plan(64, 64, splits, 32)
+        keep = []
+        dx_, ddy, dout = g.dev(x), g.dev(dys), g.dev(init)
+        d = _batched_desc(dx_, ddy, dout, True, False, M, N, K, 3, 0, K * N, gap)
+        d.bias_grad = dout.data_ptr() + 4 * M * N
+        d.bias_batch_stride = gap
+        d.beta = beta
+        _with_workspace(g, keep, d)
+        g.call("tlh_gemm", ctypes.byref(d))
+        outs.append(g.host(dout))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    for j in range(3):
+        w = outs[1][j * gap:j * gap + M * N].reshape(M, N)
+        w0 = init[j * gap:j * gap + M * N].reshape(M, N)
+        bg = outs[1][j * gap + M * N:j * gap + M * N + N]
+        bg0 = init[j * gap + M * N:j * gap + M * N + N]
+        assert_rel(w, O.matmul(x.T, dys[j]) + beta * w0, 1e-3, f"dW[{j}]")
+        assert_close(bg, O.sum_to_shape(dys[j], [N]) + beta * bg0, rtol=1e-4, atol=1e-3,
+                     what=f"db[{j}]")
 
 
 @pytest.mark.parametrize("M,N,K", [(6144, 384, 384), (100, 70, 64)])
