@@ -191,6 +191,24 @@ int tlh_matmul(const float *a, const float *b, float *c, uint32_t M, uint32_t K,
                const uint32_t *batch_shape, const uint32_t *batch_stride_a,
                const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
                void *stream);
+/* Scratch (floats) that tlh_matmul_ws can use for this product: the K-chunk
+ * partials of the tail split or of split-K (see tlh_gemm_workspace_size);
+ * 0 when the plan needs none. Takes tlh_matmul's shape and stride
+ * arguments. */
+int tlh_matmul_workspace_size(uint32_t M, uint32_t K, uint32_t N, uint32_t a_rs,
+                              uint32_t a_cs, uint32_t b_rs, uint32_t b_cs, uint32_t c_rs,
+                              uint32_t c_cs, uint32_t batch_ndim, const uint32_t *batch_shape,
+                              const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                              const uint32_t *batch_stride_c, size_t *elems);
+/* tlh_matmul with that scratch (partials summed in a fixed order: the
+ * result does not depend on the split). A null or too small workspace runs
+ * the unsplit plan of tlh_matmul. */
+int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, uint32_t K,
+                  uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs, uint32_t b_cs,
+                  uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+                  const uint32_t *batch_shape, const uint32_t *batch_stride_a,
+                  const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
+                  float *workspace, size_t workspace_elems, void *stream);
 
 /* Fused GEMM used by the program layer (no reference counterpart; it fuses
  * EXPR_LINEAR = mult + in-place bias add (execute.h:241-252), the GELU that

@@ -1095,15 +1095,17 @@ TLH_API int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems) {
   return 0;
 }
 
-TLH_API int tlh_matmul(const float *a, const float *b, float *c, uint32_t M,
-                       uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
-                       uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
-                       uint32_t batch_ndim, const uint32_t *batch_shape,
-                       const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
-                       const uint32_t *batch_stride_c, void *stream) {
+namespace {
+// tlh_matmul's strided operands -> a GemmDesc (`skip`: nothing to compute).
+int matmul_desc(const float *a, const float *b, float *c, uint32_t M, uint32_t K, uint32_t N,
+                uint32_t a_rs, uint32_t a_cs, uint32_t b_rs, uint32_t b_cs, uint32_t c_rs,
+                uint32_t c_cs, uint32_t batch_ndim, const uint32_t *batch_shape,
+                const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                const uint32_t *batch_stride_c, tlh::GemmDesc &d, bool &skip) {
+
+  skip = false;
   if (batch_ndim > 4 || c_cs != 1) return int(hipErrorInvalidValue);
-  if (M == 0 || N == 0) return 0;
-  tlh::GemmDesc d;
+  if (M == 0 || N == 0) { skip = true; return 0; }
   d.A = a; d.B = b; d.C = c;
   d.M = int(M); d.N = int(N); d.K = int(K);
   // A: row-major (column stride 1) or column-major (row stride 1).
@@ -1124,7 +1126,7 @@ TLH_API int tlh_matmul(const float *a, const float *b, float *c, uint32_t M,
     d.batch_stride_c[i] = batch_stride_c[i];
     batch *= batch_shape[i];
   }
-  if (batch == 0) return 0;
+  if (batch == 0) { skip = true; return 0; }
   if (batch > 65535) return int(hipErrorInvalidValue);
   d.batch = int(batch);
   // Collapse a batch whose right operand is shared (stride 0 on every batch
@@ -1147,5 +1149,60 @@ TLH_API int tlh_matmul(const float *a, const float *b, float *c, uint32_t M,
     d.batch_ndim = 0;
   }
   if (d.batch == 1) d.batch_ndim = 0;
+  return 0;
+}
+} // namespace
+
+#define TLH_MATMUL_ARGS                                                                   \
+  a, b, c, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, batch_ndim, batch_shape,           \
+      batch_stride_a, batch_stride_b, batch_stride_c
+
+TLH_API int tlh_matmul(const float *a, const float *b, float *c, uint32_t M,
+                       uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
+                       uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
+                       uint32_t batch_ndim, const uint32_t *batch_shape,
+                       const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                       const uint32_t *batch_stride_c, void *stream) {
+  tlh::GemmDesc d;
+  bool skip = false;
+  const int st = matmul_desc(TLH_MATMUL_ARGS, d, skip);
+  if (st || skip) return st;
   return tlh::gemm_launch(d, stream);
 }
+
+TLH_API int tlh_matmul_workspace_size(uint32_t M, uint32_t K, uint32_t N, uint32_t a_rs,
+                                      uint32_t a_cs, uint32_t b_rs, uint32_t b_cs,
+                                      uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+                                      const uint32_t *batch_shape,
+                                      const uint32_t *batch_stride_a,
+                                      const uint32_t *batch_stride_b,
+                                      const uint32_t *batch_stride_c, size_t *elems) {
+  if (!elems) return int(hipErrorInvalidValue);
+  *elems = 0;
+  const float *a = nullptr, *b = nullptr;
+  float *c = nullptr;
+  tlh::GemmDesc d;
+  bool skip = false;
+  const int st = matmul_desc(TLH_MATMUL_ARGS, d, skip);
+  if (st || skip) return st;
+  *elems = tlh::gemm_workspace_elems(d);
+  return 0;
+}
+
+TLH_API int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, uint32_t K,
+                          uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs,
+                          uint32_t b_cs, uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+                          const uint32_t *batch_shape, const uint32_t *batch_stride_a,
+                          const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
+                          float *workspace, size_t workspace_elems, void *stream) {
+  tlh::GemmDesc d;
+  bool skip = false;
+  const int st = matmul_desc(TLH_MATMUL_ARGS, d, skip);
+  if (st || skip) return st;
+  if (workspace && workspace_elems) {
+    d.workspace = workspace;
+    d.workspace_elems = workspace_elems;
+  }
+  return tlh::gemm_launch(d, stream);
+}
+#undef TLH_MATMUL_ARGS

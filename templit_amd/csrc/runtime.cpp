@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <numeric>
 #include <stdexcept>
 #include <string>
@@ -392,10 +393,28 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
     check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "mult");
     return;
   }
-  check(tlh_matmul(in(a), in(b), out(o), M, K, N, a.strides()[ra - 2], a.strides()[ra - 1],
-                   b.strides()[rb - 2], b.strides()[rb - 1], o.strides()[ro - 2],
-                   o.strides()[ro - 1], uint32_t(batch.shape.size()), batch.shape.data(),
-                   batch.sa.data(), batch.sb.data(), batch.sc.data(), stream()),
+  const uint32_t a_rs = a.strides()[ra - 2], a_cs = a.strides()[ra - 1];
+  const uint32_t b_rs = b.strides()[rb - 2], b_cs = b.strides()[rb - 1];
+  const uint32_t c_rs = o.strides()[ro - 2], c_cs = o.strides()[ro - 1];
+  const uint32_t nb = uint32_t(batch.shape.size());
+  size_t ws_elems = 0;
+  check(tlh_matmul_workspace_size(M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                                  batch.shape.data(), batch.sa.data(), batch.sb.data(),
+                                  batch.sc.data(), &ws_elems),
+        "mult");
+  if (ws_elems == 0 || ws_elems > UINT32_MAX) {
+    check(tlh_matmul(in(a), in(b), out(o), M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                     batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
+                     stream()),
+          "mult");
+    return;
+  }
+  // K-chunk partials (tail split / split-K); freed to the pool right away,
+  // which is safe because its next user is ordered after this work.
+  Tensor partials({uint32_t(ws_elems)});
+  check(tlh_matmul_ws(in(a), in(b), out(o), M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                      batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
+                      out(partials), ws_elems, stream()),
         "mult");
 }
 

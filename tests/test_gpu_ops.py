@@ -149,6 +149,42 @@ def test_matmul(g, sa, sb):
     assert_rel(mult(g, a, b), O.matmul(a, b), 1e-3, "matmul")
 
 
+@pytest.mark.parametrize("sa,sb,splits", [
+    ((6144, 1536), (1536, 384), True),          # 576 tiles: tail split over K chunks
+    ((32, 192, 1536), (1536, 384), True),       # weight broadcast, folded into one product
+    ((384, 6144), (6144, 384), True),           # 36 tiles: split-K
+    ((32, 384, 192), (32, 192, 384), False),    # per-sample weight grad: no scratch
+    ((1, 1024), (1024, 512), True),             # one row: GEMV chunks
+])
+def test_matmul_workspace(g, sa, sb, splits):
+    # tlh_matmul_ws with the scratch tlh_matmul_workspace_size asks for equals
+    # the oracle and tlh_matmul; a null workspace runs tlh_matmul's plan
+    # (bit for bit)
+    a = O.normal(sa, 12, 0, 0.5)
+    b = O.normal(sb, 13, 0, 0.5)
+    M, K, N = sa[-2], sa[-1], sb[-1]
+    batch = list(sa[:-2])
+    sa_ = [M * K] if batch else [0]
+    sb_ = [K * N] if len(sb) > 2 else [0]  # 0: B broadcast over the batch
+    sc = [M * N] if batch else [0]
+    shape = u32(batch or [1])
+    args = (M, K, N, K, 1, N, 1, N, 1, len(batch), shape, u32(sa_), u32(sb_), u32(sc))
+    n = ctypes.c_size_t()
+    check(g.lib.tlh_matmul_workspace_size(*args, ctypes.byref(n)), "matmul_workspace_size")
+    assert (n.value > 0) == splits
+    da, db = g.dev(a), g.dev(b)
+    ws = g.empty((max(1, n.value),))
+    outs = []
+    for workspace, elems in ((ws.data_ptr(), n.value), (None, 0)):
+        out = g.empty(batch + [M, N])
+        g.call("tlh_matmul_ws", da, db, out, *args, workspace, elems)
+        outs.append(g.host(out))
+    plain = mult(g, a, b)
+    np.testing.assert_array_equal(outs[1], plain)
+    assert_rel(outs[0], O.matmul(a, b), 1e-3, "matmul_ws")
+    assert_rel(outs[0], plain, 1e-5, "matmul_ws vs matmul")
+
+
 def test_matmul_kat_and_identity(g):
     # test_metal_runtime.cpp:281-342
     a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
