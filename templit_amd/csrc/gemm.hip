@@ -204,20 +204,64 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
   const bool raw = b.partial || p.splits > 1;
   const int rs = b.partial ? BN : p.N;
   float *rbase = b.partial ? b.C - (size_t(b.m0) * BN + b.n0) : b.C;
+  // (the gathered path is kept to waves with at most two accumulator tiles:
+  // with four, the unrolled epilogue no longer fits and spills)
+  const bool reads = TM * TN <= 2 &&
+                     (p.beta != 0.0f || p.residual != nullptr || p.epilogue == kEpiGeluBwd);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = b.n0 + wn * WN + j * 32 + r;
       if (!FULL && n >= p.N) continue;
+      const int mb = b.m0 + wm * WM + i * 32 + 4 * hk;
+      if (raw || !reads) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = b.m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
-        if (!FULL && m >= p.M) continue;
-        if (raw) {
-          rbase[size_t(m) * rs + n] = acc[i][j][v];
-        } else {
-          epilogue_store(p, b.bias, b.C, m, n, acc[i][j][v]);
+        for (int v = 0; v < 16; ++v) {
+          const int m = mb + 8 * (v >> 2) + (v & 3);
+          if (!FULL && m >= p.M) continue;
+          if (raw) {
+            rbase[size_t(m) * rs + n] = acc[i][j][v];
+          } else {
+            epilogue_store(p, b.bias, b.C, m, n, acc[i][j][v]);
+          }
+        }
+      } else if constexpr (TM * TN <= 2) {
+        // The epilogue reads C, the residual or the GELU pre-activation. Each
+        // group of 4 rows loads its operands before its first store:
+        // interleaved, every load would wait behind the previous element's
+        // store (which might alias it), one memory latency per element. Same
+        // arithmetic, same order as epilogue_store.
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float cold[4], res[4], ax[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = mb + 8 * g + e;
+            cold[e] = res[e] = ax[e] = 0.f;
+            if (!FULL && m >= p.M) continue;
+            const size_t idx = out_index(p, m, n);
+            if (p.beta != 0.0f) cold[e] = b.C[idx];
+            if (p.residual) res[e] = p.residual[idx];
+            if (p.epilogue == kEpiGeluBwd) ax[e] = p.aux[idx];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = mb + 8 * g + e;
+            if (!FULL && m >= p.M) continue;
+            const size_t idx = out_index(p, m, n);
+            float x = acc[i][j][4 * g + e];
+            if (b.bias) x += b.bias[n];
+            if (p.beta != 0.0f) x += p.beta * cold[e];
+            if (p.residual) x += res[e];
+            if (p.epilogue == kEpiGelu) {
+              p.aux[idx] = x;
+              x = gelu_fwd(x);
+            } else if (p.epilogue == kEpiGeluBwd) {
+              x *= gelu_grad(ax[e]);
+            }
+            b.C[idx] = x;
+          }
         }
       }
     }
