@@ -228,16 +228,18 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
         }
       } else if constexpr (TM * TN <= 2) {
         // The epilogue reads C, the residual or the GELU pre-activation. Each
-        // group of 4 rows loads its operands before its first store:
+        // group of rows loads its operands before its first store:
         // interleaved, every load would wait behind the previous element's
         // store (which might alias it), one memory latency per element. Same
-        // arithmetic, same order as epilogue_store.
+        // arithmetic, same order as epilogue_store. GS rows per group: all 16
+        // with one accumulator tile per wave, 4 with two.
+        constexpr int GS = TM * TN == 1 ? 16 : 4;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float cold[4], res[4], ax[4];
+        for (int g = 0; g < 16 / GS; ++g) {
+          float cold[GS], res[GS], ax[GS];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = mb + 8 * g + e;
+          for (int e = 0; e < GS; ++e) {
+            const int v = g * GS + e, m = mb + 8 * (v >> 2) + (v & 3);
             cold[e] = res[e] = ax[e] = 0.f;
             if (!FULL && m >= p.M) continue;
             const size_t idx = out_index(p, m, n);
@@ -246,11 +248,11 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
             if (p.epilogue == kEpiGeluBwd) ax[e] = p.aux[idx];
           }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = mb + 8 * g + e;
+          for (int e = 0; e < GS; ++e) {
+            const int v = g * GS + e, m = mb + 8 * (v >> 2) + (v & 3);
             if (!FULL && m >= p.M) continue;
             const size_t idx = out_index(p, m, n);
-            float x = acc[i][j][4 * g + e];
+            float x = acc[i][j][v];
             if (b.bias) x += b.bias[n];
             if (p.beta != 0.0f) x += p.beta * cold[e];
             if (p.residual) x += res[e];
