@@ -80,6 +80,17 @@ int tlg_set_lr(void *program, float lr);
 int tlg_set_concurrency(void *program, int mode);
 int tlg_get_concurrency(void *program, int *two_streams);
 
+/* Weight layout of the forward products (no counterpart in the reference):
+ * 1 runs them on K-contiguous copies of the weight matrices, rebuilt from
+ * the weights by one transpose launch at the start of every forward (so
+ * writes through tlg_param_info pointers are seen), 0 on the [in, out]
+ * weights themselves, -1 (the default at tlg_create) picks 1 while the
+ * [batch*seq, dim] products have fewer than 4 tiles of 64x64 per compute
+ * unit and 0 above. Results are bitwise the same either way.
+ * Applies to forwards issued or captured after the call. */
+int tlg_set_forward_copies(void *program, int mode);
+int tlg_get_forward_copies(void *program, int *copies);
+
 /* Device buffers the step reads its batch from (uint32 [B*T] each) and
  * writes per-row losses to (float [B*T]); stable for the program's life. */
 int tlg_io(void *program, uint32_t **tokens, uint32_t **targets, float **losses,

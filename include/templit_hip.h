@@ -167,6 +167,21 @@ int tlh_copy(const float *a, float *out, size_t n, void *stream);
 int tlh_gelu_backward(const float *grad, const float *x, float *out, size_t n,
                       void *stream);
 
+/* Many row-major matrices transposed in one launch (no counterpart in the
+ * reference: the GPT step program keeps K-contiguous copies of its weights
+ * for the forward products with it). Job i transposes the rows x cols
+ * matrix at src + src_offset into the cols x rows matrix at dst +
+ * dst_offset; first_tile is the number of 64x64 output tiles of the jobs
+ * before it and total_tiles the sum over all jobs. `jobs` is a device array
+ * of `count` <= 256 entries; sources and destinations must not overlap. */
+typedef struct tlh_transpose_job {
+  uint64_t src_offset, dst_offset;
+  uint32_t rows, cols;
+  uint32_t first_tile, reserved;
+} tlh_transpose_job;
+int tlh_transpose_multi(const float *src, float *dst, const tlh_transpose_job *jobs,
+                        uint32_t count, uint32_t total_tiles, void *stream);
+
 /* transpose (math.metal:566-584, runtime.cpp:529-569): `out` is contiguous
  * with `ndim` dims `out_shape`; in_strides are the input's strides with the
  * two swapped axes exchanged (runtime.cpp:549-553). Any permutation of

@@ -264,17 +264,11 @@ __global__ __launch_bounds__(256) void gather4_kernel(const f4 *__restrict__ a,
 // Batched 2-D transpose through a padded 64x64 LDS tile:
 // out[z, i, j] = a[z*batch_stride + j*ld_in + i] with out [z, rows, cols]
 // row-major (rows = input columns).
-__global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__restrict__ a,
-                                                              float *__restrict__ out,
-                                                              uint32_t rows, uint32_t cols,
-                                                              size_t in_batch_stride,
-                                                              uint32_t ld_in) {
-  __shared__ float tile[64][65];
-  const uint32_t z = blockIdx.z;
-  const uint32_t i0 = blockIdx.y * 64; // output row block (= input column block)
-  const uint32_t j0 = blockIdx.x * 64; // output column block (= input row block)
-  const float *src = a + size_t(z) * in_batch_stride;
-  float *dst = out + size_t(z) * rows * cols;
+// One 64x64 tile of out[rows][cols] = in^T, in = src[cols][rows] with row
+// pitch ld_in; i0 / j0 = the tile's first output row / column.
+__device__ inline void transpose_tile(const float *__restrict__ src, float *__restrict__ dst,
+                                      uint32_t rows, uint32_t cols, uint32_t ld_in,
+                                      uint32_t i0, uint32_t j0, float (&tile)[64][65]) {
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   // all 16 loads of a thread in flight before the LDS writes
   float v[16];
@@ -291,6 +285,41 @@ __global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__res
     const uint32_t o_row = i0 + ty + 4 * i, o_col = j0 + tx;
     if (o_row < rows && o_col < cols) dst[size_t(o_row) * cols + o_col] = tile[tx][ty + 4 * i];
   }
+}
+
+__global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__restrict__ a,
+                                                              float *__restrict__ out,
+                                                              uint32_t rows, uint32_t cols,
+                                                              size_t in_batch_stride,
+                                                              uint32_t ld_in) {
+  __shared__ float tile[64][65];
+  const uint32_t z = blockIdx.z;
+  transpose_tile(a + size_t(z) * in_batch_stride, out + size_t(z) * rows * cols, rows, cols,
+                 ld_in, blockIdx.y * 64, blockIdx.x * 64, tile);
+}
+
+// Block b handles output tile b - first_tile of the job whose tile range
+// holds b; the threads test one job each to find it.
+__global__ __launch_bounds__(256) void transpose_multi_kernel(const float *__restrict__ src,
+                                                              float *__restrict__ dst,
+                                                              const tlh_transpose_job *jobs,
+                                                              uint32_t count,
+                                                              uint32_t total_tiles) {
+  __shared__ float tile[64][65];
+  __shared__ uint32_t which;
+  const uint32_t b = blockIdx.x;
+  const uint32_t t = threadIdx.x;
+  if (t < count) {
+    const uint32_t end = t + 1 < count ? jobs[t + 1].first_tile : total_tiles;
+    if (jobs[t].first_tile <= b && b < end) which = t;
+  }
+  __syncthreads();
+  const tlh_transpose_job j = jobs[which];
+  // output [j.cols][j.rows] = source [j.rows][j.cols] transposed
+  const uint32_t tiles_x = (j.rows + 63) / 64;
+  const uint32_t local = b - j.first_tile;
+  transpose_tile(src + j.src_offset, dst + j.dst_offset, j.cols, j.rows, j.cols,
+                 (local / tiles_x) * 64, (local % tiles_x) * 64, tile);
 }
 
 } // namespace
@@ -356,6 +385,15 @@ TLH_API int tlh_gelu_backward(const float *grad, const float *x, float *out, siz
   const size_t n4 = (aligned16(grad) && aligned16(x) && aligned16(out)) ? n / 4 : 0;
   gelu_backward_kernel<<<stride_grid(n4 ? n4 : n, 256), 256, 0, as_stream(stream)>>>(
       grad, x, out, n4, n);
+  return launch_status();
+}
+
+TLH_API int tlh_transpose_multi(const float *src, float *dst, const tlh_transpose_job *jobs,
+                                uint32_t count, uint32_t total_tiles, void *stream) {
+  if (count == 0 || total_tiles == 0) return 0;
+  if (count > 256 || !src || !dst || !jobs) return int(hipErrorInvalidValue);
+  transpose_multi_kernel<<<total_tiles, 256, 0, as_stream(stream)>>>(src, dst, jobs, count,
+                                                                     total_tiles);
   return launch_status();
 }
 

@@ -100,7 +100,17 @@ struct Program {
   double gemm_flops = 0.0, gemm_bytes = 0.0;
   std::vector<tlh_gemm_desc> gemm_descs; // the profiled step's GEMMs, in launch order
 
+  // K-contiguous copies of the weight matrices ([out, in], at the weights'
+  // own offsets) for the forward products, rebuilt from the weights at the
+  // start of every forward by one tlh_transpose_multi launch; see
+  // auto_forward_copies.
+  float *wt = nullptr;
+  void *wt_jobs = nullptr;
+  uint32_t wt_count = 0, wt_tiles = 0;
+  bool forward_copies = false;
+
   float *P(uint32_t i) const { return params + offset[i]; }
+  float *PT(uint32_t i) const { return wt + offset[i]; }
   float *G(uint32_t i) const { return grads + offset[i]; }
 };
 
@@ -151,6 +161,14 @@ tlh_gemm_desc desc(const float *a, const float *b, float *c, int m, int n, int k
   d.ldb = tb ? k : n;
   d.ldc = n;
   return d;
+}
+
+// The forward product rows x weight w ([k, n]): on the K-contiguous copy
+// (B transposed) when the program keeps copies, else on the weight itself.
+tlh_gemm_desc wdesc(const Program &p, bool copies, const float *a, uint32_t w, float *c, int m,
+                    int n, int k) {
+  return copies ? desc(a, p.PT(w), c, m, n, k, false, true)
+                : desc(a, p.P(w), c, m, n, k, false, false);
 }
 
 #define TRY(x)                                                                                 \
@@ -223,6 +241,15 @@ bool auto_two_streams(const Program &p) {
   return tiles < 4 * size_t(cus);
 }
 
+// Forward products on K-contiguous weight copies (B transposed) instead of
+// the [in, out] weights: the GEMM reads a K-contiguous operand tile from LDS
+// with one ds_read_b128 per fragment instead of four ds_read_b32, and one
+// launch per forward rebuilds the copies. Measured on MI355X: rows 6144 x
+// dim 384 (64x64 tiles, fewer than 4 per CU) 3.697 -> 3.679 ms per step;
+// rows 8192 x dim 1024 unchanged (77.7 ms), so the copies are used below 4
+// tiles per CU only, the same rule as the second stream.
+bool auto_forward_copies(const Program &p) { return p.wt != nullptr && auto_two_streams(p); }
+
 // The side stream continues from the main stream's current point.
 int fork(Program &p, void *ev) {
   if (!concurrent(p)) return 0;
@@ -275,6 +302,12 @@ int forward(Program &p, uint32_t seq) {
   const tlg_config &c = p.cfg;
   const size_t rows = size_t(c.batch) * seq;
   const int R = int(rows), D = int(c.dim), F = int(c.ffn), V = int(c.vocab);
+  // (one-row products keep the weights: the GEMV path reads B row-major)
+  const bool copies = p.forward_copies && rows > 1;
+  if (copies) {
+    TRY(tlh_transpose_multi(p.params, p.wt, static_cast<const tlh_transpose_job *>(p.wt_jobs),
+                            p.wt_count, p.wt_tiles, p.stream));
+  }
   TRY(tlh_embedding_add_positions(p.P(0), c.vocab, p.P(1), p.tokens, c.batch, seq, c.dim,
                                   p.x[0], p.stream));
   for (uint32_t l = 0; l < c.layers; ++l) {
@@ -284,7 +317,7 @@ int forward(Program &p, uint32_t seq) {
       // Q, K and V in one batched launch: the three weights (and biases)
       // sit at a constant stride in the parameter buffer and q, k, v are
       // consecutive planes of one allocation.
-      tlh_gemm_desc d = desc(p.n1[l], p.P(w), p.q[l], R, D, D, false, false);
+      tlh_gemm_desc d = wdesc(p, copies, p.n1[l], w, p.q[l], R, D, D);
       d.bias = p.P(w + 1);
       d.remap_t = int(seq);
       d.remap_h = int(c.heads);
@@ -302,21 +335,21 @@ int forward(Program &p, uint32_t seq) {
                                    p.stream);
     }));
     {
-      tlh_gemm_desc d = desc(p.o[l], p.P(w + 6), p.x_mid[l], R, D, D, false, false);
+      tlh_gemm_desc d = wdesc(p, copies, p.o[l], w + 6, p.x_mid[l], R, D, D);
       d.bias = p.P(w + 7);
       d.residual = p.x[l];
       TRY(gemm(p, d));
     }
     TRY(tlh_rms_norm(p.x_mid[l], nullptr, p.n2[l], nullptr, rows, c.dim, kRmsEps, p.stream));
     {
-      tlh_gemm_desc d = desc(p.n2[l], p.P(w + 8), p.g[l], R, F, D, false, false);
+      tlh_gemm_desc d = wdesc(p, copies, p.n2[l], w + 8, p.g[l], R, F, D);
       d.bias = p.P(w + 9);
       d.epilogue = TLH_EPI_GELU;
       d.aux = p.u[l];
       TRY(gemm(p, d));
     }
     {
-      tlh_gemm_desc d = desc(p.g[l], p.P(w + 10), p.x[l + 1], R, D, F, false, false);
+      tlh_gemm_desc d = wdesc(p, copies, p.g[l], w + 10, p.x[l + 1], R, D, F);
       d.bias = p.P(w + 11);
       d.residual = p.x_mid[l];
       TRY(gemm(p, d));
@@ -324,7 +357,7 @@ int forward(Program &p, uint32_t seq) {
   }
   TRY(tlh_rms_norm(p.x[c.layers], nullptr, p.nf, nullptr, rows, c.dim, kRmsEps, p.stream));
   const uint32_t last = 2 + 12 * c.layers;
-  tlh_gemm_desc d = desc(p.nf, p.P(last), p.logits, R, V, D, false, false);
+  tlh_gemm_desc d = wdesc(p, copies, p.nf, last, p.logits, R, V, D);
   d.bias = p.P(last + 1);
   return gemm(p, d);
 }
@@ -536,6 +569,37 @@ int create(Program &p) {
     TRY(tlh_memcpy_h2d(p.tab_sizes, sz.data(), count * sizeof(uint64_t), p.stream));
     TRY(tlh_stream_synchronize(p.stream));
   }
+  {
+    // the weight matrices [in, out]: per layer wq, wk, wv, wo, w1, w2, then wp
+    std::vector<tlh_transpose_job> jobs;
+    std::vector<uint32_t> weights;
+    for (uint32_t l = 0; l < c.layers; ++l)
+      for (uint32_t k : {0u, 2u, 4u, 6u, 8u, 10u}) weights.push_back(2 + 12 * l + k);
+    weights.push_back(2 + 12 * uint32_t(L));
+    uint32_t tiles = 0;
+    for (uint32_t w : weights) {
+      const uint32_t in = w == 2 + 12 * uint32_t(L) ? uint32_t(D)
+                          : (w - 2) % 12 == 10  ? uint32_t(F)
+                                                : uint32_t(D);
+      const uint32_t out = uint32_t(p.size[w] / in);
+      tlh_transpose_job j{};
+      j.src_offset = j.dst_offset = p.offset[w];
+      j.rows = in;
+      j.cols = out;
+      j.first_tile = tiles;
+      tiles += ((in + 63) / 64) * ((out + 63) / 64);
+      jobs.push_back(j);
+    }
+    if (jobs.size() <= 256) {
+      TRY(allocf(p, &p.wt, p.padded_total));
+      TRY(alloc(p, &p.wt_jobs, jobs.size() * sizeof(tlh_transpose_job)));
+      TRY(tlh_memcpy_h2d(p.wt_jobs, jobs.data(), jobs.size() * sizeof(tlh_transpose_job),
+                         p.stream));
+      TRY(tlh_stream_synchronize(p.stream));
+      p.wt_count = uint32_t(jobs.size());
+      p.wt_tiles = tiles;
+    }
+  }
   TRY(tlh_fill_u32(p.steps, 0, count, p.stream));
   TRY(tlh_fill_f32(p.params, 0.0f, p.padded_total, p.stream));
   TRY(tlh_fill_f32(p.grads, 0.0f, p.padded_total, p.stream));
@@ -636,6 +700,7 @@ int create(Program &p) {
   }
   TRY(tlh_stream_create(&p.side));
   p.two_streams = auto_two_streams(p);
+  p.forward_copies = auto_forward_copies(p);
   p.sync.resize(2 + 8 * L);
   for (auto &e : p.sync) TRY(tlh_event_create(&e));
   p.lr = 1e-3f;
@@ -842,6 +907,20 @@ int tlg_set_concurrency(void *program, int mode) {
   TRY(tlh_stream_synchronize(p->stream));
   TRY(tlh_stream_synchronize(p->side));
   p->two_streams = mode < 0 ? auto_two_streams(*p) : mode == 1;
+  return 0;
+}
+
+int tlg_set_forward_copies(void *program, int mode) {
+  Program *p = static_cast<Program *>(program);
+  if (mode < -1 || mode > 1) return kInvalidValue;
+  if (mode == 1 && !p->wt) return kInvalidValue;
+  TRY(tlh_stream_synchronize(p->stream));
+  p->forward_copies = mode < 0 ? auto_forward_copies(*p) : mode == 1;
+  return 0;
+}
+
+int tlg_get_forward_copies(void *program, int *copies) {
+  *copies = static_cast<Program *>(program)->forward_copies ? 1 : 0;
   return 0;
 }
 

@@ -100,6 +100,7 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_copy": [P, P, c_size_t, P],
     "tlh_gelu_backward": [P, P, P, c_size_t, P],
     "tlh_transpose": [P, P, c_uint32, U32P, U32P, P],
+    "tlh_transpose_multi": [P, P, P, c_uint32, c_uint32, P],
     # products
     "tlh_matmul": [P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                    c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P, U32P, P],
@@ -224,6 +225,8 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_set_lr": [P, c_float],
     "tlg_set_concurrency": [P, c_int],
     "tlg_get_concurrency": [P, POINTER(c_int)],
+    "tlg_set_forward_copies": [P, c_int],
+    "tlg_get_forward_copies": [P, POINTER(c_int)],
     "tlg_io": [P, FP, FP, FP, FP],
     "tlg_train_step": [P, c_float, c_float, c_int],
     "tlg_forward": [P],
@@ -437,6 +440,16 @@ class GptProgram:
         check(self.lib.tlg_set_concurrency(self.handle, int(mode)), "tlg_set_concurrency")
         out = c_int()
         check(self.lib.tlg_get_concurrency(self.handle, ctypes.byref(out)), "tlg_get_concurrency")
+        return bool(out.value)
+
+    def set_forward_copies(self, mode):
+        """-1 automatic (the default), 0 forward products on the [in, out]
+        weights, 1 on K-contiguous copies rebuilt at each forward; returns
+        whether the forward now uses the copies."""
+        check(self.lib.tlg_set_forward_copies(self.handle, int(mode)), "tlg_set_forward_copies")
+        out = c_int()
+        check(self.lib.tlg_get_forward_copies(self.handle, ctypes.byref(out)),
+              "tlg_get_forward_copies")
         return bool(out.value)
 
     def train_step(self, root_grad, max_norm, update=True):

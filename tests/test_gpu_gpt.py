@@ -203,6 +203,35 @@ def test_stream_choice_follows_the_tile_count():
         prog.close()
 
 
+def test_forward_copies_change_no_bit():
+    # forward products on K-contiguous weight copies (rebuilt at every
+    # forward) against the [in, out] weights: the same products in the same
+    # order, so losses, gradients and updated parameters agree bitwise;
+    # a parameter written through its device pointer between steps is seen
+    prog = GptProgram(256, 192, 384, 6, 2, 4)
+    try:
+        runs = []
+        for mode in (0, 1):
+            assert prog.set_forward_copies(mode) == bool(mode)
+            prog.init_params(seed=5, std=0.02)
+            prog.set_optimizer(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+            prog.random_batch(seed=6)
+            for _ in range(2):
+                prog.train_step(1.0 / (4 * 192), 1.0)
+            params = prog.get_params()
+            params[: params.size // 2] *= 1.5
+            prog.set_params(params)
+            prog.train_step(1.0 / (4 * 192), 1.0)
+            prog.synchronize()
+            runs.append((prog.losses(), prog.get_grads(), prog.get_params()))
+        for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
+            assert np.array_equal(got, want), what
+        with pytest.raises(NativeError):
+            prog.set_forward_copies(2)
+    finally:
+        prog.close()
+
+
 def read_archive(path):
     """name -> bytes of a checkpoint archive file (u32 name length, name,
     u32 blob length, blob)*."""

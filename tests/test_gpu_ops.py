@@ -113,6 +113,38 @@ def test_transpose(g, shape, da, db):
     np.testing.assert_array_equal(g.host(out), expect)  # a permutation is exact
 
 
+JOB = np.dtype([("src", "<u8"), ("dst", "<u8"), ("rows", "<u4"), ("cols", "<u4"),
+                ("first_tile", "<u4"), ("reserved", "<u4")])
+
+
+def test_transpose_multi(g):
+    # ragged shapes (partial 64x64 tiles, a single row, a single column),
+    # destinations in another order than the sources
+    shapes = [(384, 384), (384, 1536), (1536, 384), (100, 70), (1, 5), (65, 129), (7, 1)]
+    offs, off = [], 0
+    for r, c in shapes:
+        offs.append(off)
+        off += (r * c + 63) // 64 * 64
+    src = O.normal((off,), 31)
+    dst_offs, off2 = [], 0  # the destinations laid out in reverse order
+    for r, c in reversed(shapes):
+        dst_offs.append(off2)
+        off2 += (r * c + 63) // 64 * 64
+    dst_offs = list(reversed(dst_offs))
+    jobs = np.zeros(len(shapes), JOB)
+    tiles = 0
+    for i, ((r, c), so, do) in enumerate(zip(shapes, offs, dst_offs)):
+        jobs[i] = (so, do, r, c, tiles, 0)
+        tiles += ((r + 63) // 64) * ((c + 63) // 64)
+    dev_jobs = torch.from_numpy(jobs.view(np.uint8).copy()).to("cuda")
+    out = g.zeros((off2,))
+    g.call("tlh_transpose_multi", g.dev(src), out, dev_jobs, len(shapes), tiles)
+    got = g.host(out)
+    for (r, c), so, do in zip(shapes, offs, dst_offs):
+        want = src[so:so + r * c].reshape(r, c).T
+        np.testing.assert_array_equal(got[do:do + r * c].reshape(c, r), want)
+
+
 # ---------------------------------------------------------------------------
 # matmul
 # ---------------------------------------------------------------------------
