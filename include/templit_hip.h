@@ -173,7 +173,10 @@ int tlh_gelu_backward(const float *grad, const float *x, float *out, size_t n,
  * matrix at src + src_offset into the cols x rows matrix at dst +
  * dst_offset; first_tile is the number of 64x64 output tiles of the jobs
  * before it and total_tiles the sum over all jobs. `jobs` is a device array
- * of `count` <= 256 entries; sources and destinations must not overlap. */
+ * of `count` <= 256 entries; sources and destinations must not overlap.
+ * Tiles past the last job's own (total_tiles larger than the sum) write
+ * nothing; a table whose first_tile values descend (or exceed total_tiles)
+ * is inconsistent, and then the launch writes nothing at all. */
 typedef struct tlh_transpose_job {
   uint64_t src_offset, dst_offset;
   uint32_t rows, cols;

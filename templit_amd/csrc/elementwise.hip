@@ -300,25 +300,31 @@ __global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__res
 
 // Block b handles output tile b - first_tile of the job whose tile range
 // holds b; the threads test one job each to find it. A block that no job
-// claims (an inconsistent table) does nothing, and transpose_tile keeps
-// every access inside the job's own rows x cols.
+// claims does nothing, and transpose_tile keeps every access inside the
+// job's own rows x cols (so blocks past the last job's tiles write
+// nothing). A table whose first_tile values descend anywhere would let two
+// jobs claim one block: every block then exits and nothing is written.
 __global__ __launch_bounds__(256) void transpose_multi_kernel(const float *__restrict__ src,
                                                               float *__restrict__ dst,
                                                               const tlh_transpose_job *jobs,
                                                               uint32_t count,
                                                               uint32_t total_tiles) {
   __shared__ float tile[64][65];
-  __shared__ int which;
+  __shared__ int which, descending;
   const uint32_t b = blockIdx.x;
   const uint32_t t = threadIdx.x;
-  if (t == 0) which = -1;
+  if (t == 0) {
+    which = -1;
+    descending = 0;
+  }
   __syncthreads();
   if (t < count) {
     const uint32_t end = t + 1 < count ? jobs[t + 1].first_tile : total_tiles;
-    if (jobs[t].first_tile <= b && b < end) which = int(t);
+    if (end < jobs[t].first_tile) descending = 1;
+    else if (jobs[t].first_tile <= b && b < end) which = int(t);
   }
   __syncthreads();
-  if (which < 0) return;
+  if (which < 0 || descending) return;
   const tlh_transpose_job j = jobs[which];
   // output [j.cols][j.rows] = source [j.rows][j.cols] transposed
   const uint32_t tiles_x = (j.rows + 63) / 64;

@@ -46,6 +46,13 @@ struct Context {
   int *compare_scratch = nullptr;
   std::mutex mu;
   std::unordered_map<size_t, std::vector<void *>> free_blocks;
+  // Blocks released while the stream is being captured, with their size
+  // class. They rejoin free_blocks only once the captured graph has been
+  // launched (or the capture dropped): a record-time host write into a
+  // block handed out again within the same capture would otherwise be
+  // overwritten when the graph runs the kernels that used it first.
+  bool defer = false;
+  std::vector<std::pair<size_t, void *>> deferred;
   MemoryStats stats;
   std::vector<void *> stage_host;
   std::vector<void *> stage_event;
@@ -66,6 +73,11 @@ void free_cached(Context &c) {
     c.stats.cached_bytes -= bytes * blocks.size();
   }
   c.free_blocks.clear();
+}
+
+void pool_deferred(Context &c) {
+  for (auto &[cls, p] : c.deferred) c.free_blocks[cls].push_back(p);
+  c.deferred.clear();
 }
 
 // The stream a host transfer goes on: the main stream, or the side stream
@@ -114,6 +126,7 @@ void shutdown() {
   tlh_stream_synchronize(c.side);
   {
     std::lock_guard<std::mutex> pool_lock(c.mu);
+    pool_deferred(c);
     free_cached(c);
   }
   for (int i = 0; i < kStageSlots; ++i) {
@@ -196,12 +209,33 @@ void release(void *ptr, size_t bytes) noexcept {
   const size_t cls = size_class(bytes);
   std::lock_guard<std::mutex> lock(c.mu);
   try {
-    c.free_blocks[cls].push_back(ptr);
+    if (c.defer)
+      c.deferred.emplace_back(cls, ptr);
+    else
+      c.free_blocks[cls].push_back(ptr);
     c.stats.cached_bytes += cls;
   } catch (...) {
     tlh_free(ptr);
   }
   c.stats.in_use_bytes -= cls;
+}
+
+void defer_releases(bool on) noexcept {
+  if (!g_ctx) return;
+  Context &c = *g_ctx;
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.defer = on;
+  if (!on) {
+    try {
+      pool_deferred(c);
+    } catch (...) { // out of host memory: hand the blocks back to HIP instead
+      for (auto &[cls, p] : c.deferred) {
+        tlh_free(p);
+        c.stats.cached_bytes -= cls;
+      }
+      c.deferred.clear();
+    }
+  }
 }
 
 void write(void *dst, const void *src, size_t bytes) {

@@ -174,6 +174,7 @@ void Runtime::start() {
     // queued earlier may still be running when they do.
     check(tlh_stream_synchronize(stream()), "hipStreamSynchronize");
     check(tlh_graph_begin_capture_relaxed(stream()), "hipStreamBeginCapture");
+    hip::detail::defer_releases(true);
     s.capturing = true;
     s.signature = 0xcbf29ce484222325ull;
   }
@@ -191,6 +192,7 @@ void Runtime::submit() {
   int st = tlh_graph_end_capture_graph(stream(), &graph);
   if (st != 0) {
     s.submitted = false;
+    hip::detail::defer_releases(false);
     check(st, "hipStreamEndCapture");
   }
   s.stats.captures += 1;
@@ -208,6 +210,10 @@ void Runtime::submit() {
   }
   tlh_graph_free(graph);
   if (st == 0) st = tlh_graph_launch(exec, stream());
+  // Blocks released during the capture may be reused from here on: later
+  // work is queued after the graph, and the next capture's start() waits
+  // for the graph before any record-time host transfer.
+  hip::detail::defer_releases(false);
   if (st != 0) {
     s.submitted = false;
     check(st, "hipGraphLaunch");
@@ -227,6 +233,7 @@ void Runtime::abort() noexcept {
   if (s.capturing) {
     void *graph = nullptr;
     if (tlh_graph_end_capture_graph(stream(), &graph) == 0) tlh_graph_free(graph);
+    hip::detail::defer_releases(false); // the dropped graph never runs
     s.capturing = false;
   }
   s.recording = false;
@@ -409,8 +416,9 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
           "mult");
     return;
   }
-  // K-chunk partials (tail split / split-K); freed to the pool right away,
-  // which is safe because its next user is ordered after this work.
+  // K-chunk partials (tail split / split-K), returned to the pool on exit:
+  // their next user is queued after this work, and while a graph is being
+  // captured the pool holds released blocks back until the graph launches.
   Tensor partials({uint32_t(ws_elems)});
   check(tlh_matmul_ws(in(a), in(b), out(o), M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
                       batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
@@ -511,8 +519,8 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
           "sum_to_shape");
     return;
   }
-  // Row-chunk partials of a tall column sum; freed to the pool right away,
-  // which is safe because its next user is ordered after this work.
+  // Row-chunk partials of a tall column sum, returned to the pool on exit
+  // (stream-ordered reuse; held back while a graph is being captured).
   Tensor partials({uint32_t(ws_elems)});
   check(tlh_sum_to_shape_ws(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(),
                             out(partials), ws_elems, stream()),
@@ -803,8 +811,8 @@ void Runtime::causal_attention_backward(const Tensor &q, const Tensor &k, const 
   require_lse(lse, d);
   note(kAttentionBackward, q.shape());
   if (q.numel() == 0) return;
-  // Per-row dot(dO, O) workspace; freed to the pool right away, which is
-  // safe because its next user is ordered after this work on the stream.
+  // Per-row dot(dO, O) workspace, returned to the pool on exit
+  // (stream-ordered reuse; held back while a graph is being captured).
   Tensor delta({d.b, d.h, d.t});
   check(tlh_attention_backward(in(q), in(k), in(v), in(o), in(grad_out), in(lse), out(delta),
                                out(grad_q), out(grad_k), out(grad_v), d.b, d.h, d.t, d.d, scale, 1,

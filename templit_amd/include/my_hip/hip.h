@@ -50,6 +50,12 @@ namespace detail {
 // work has finished.
 void *allocate(size_t bytes);
 void release(void *ptr, size_t bytes) noexcept;
+// While on (hip::Runtime turns it on for a graph capture), released blocks
+// are held back from reuse; turning it off returns them to the pool. A
+// captured graph runs after record-time host writes, so a block that one
+// captured kernel used and a later tensor of the same capture received
+// would have that tensor's recorded contents overwritten at launch.
+void defer_releases(bool on) noexcept;
 
 // Host <-> device transfers, synchronous for the host (the host buffer may
 // be reused on return) and ordered after the work already on the stream.

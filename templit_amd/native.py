@@ -380,14 +380,6 @@ class GptProgram:
               "tlg_get_moments")
         return a, b
 
-    def set_batch(self, tokens, targets):
-        hip = load_hip()
-        for arr, ptr in ((tokens, self.tokens_ptr), (targets, self.targets_ptr)):
-            a = self._np.ascontiguousarray(arr, dtype=self._np.uint32)
-            assert a.size == self.rows
-            check(hip.tlh_memcpy_h2d(ptr, a.ctypes.data, a.nbytes, self.stream), "h2d")
-            check(hip.tlh_stream_synchronize(self.stream), "sync")
-
     def random_batch(self, seed):
         hip = load_hip()
         check(hip.tlh_fill_uniform_u32(self.tokens_ptr, self.rows, seed, self.cfg.vocab,

@@ -12,6 +12,7 @@
 #include "RTensor/infer_shape.h"
 #include "my_hip/runtime.h"
 #include "optimiser/AdamW.h"
+#include "templit_hip.h"
 
 #include <cmath>
 #include <cstring>
@@ -571,6 +572,68 @@ void graph_mode(hip::Runtime &rt) {
   rt.set_graph_mode(false);
 }
 
+// Graph mode with pool scratch: a split-K product releases its K-chunk
+// partials during the capture; a tensor of the same size class created
+// later in that capture and written from the host at record time must keep
+// its contents when the graph runs the product.
+void graph_mode_scratch_is_not_reused_within_a_capture(hip::Runtime &rt) {
+  constexpr uint32_t M = 384, K = 6144, N = 384; // 36 tiles: split over K
+  const uint32_t one = 1, none = 0;
+  size_t ws = 0;
+  hip::detail::check(tlh_matmul_workspace_size(M, K, N, K, 1, N, 1, N, 1, 1, &one, &none, &none,
+                                               &none, &ws),
+                     "workspace size");
+  CHECK(ws > 0);
+  Tensor a({M, K}), b({K, N}), prod({M, N}), out({uint32_t(ws)});
+  a.set(random_values(a.numel(), 21));
+  b.set(random_values(b.numel(), 22));
+  const auto values = random_values(ws, 23);
+  rt.set_graph_mode(true);
+  for (int i = 0; i < 2; ++i) {
+    run(rt, [&] {
+      rt.mult(a, b, prod);
+      Tensor c({uint32_t(ws)}); // same size class as the released partials
+      c.set(values);            // lands at record time (EXPR_CONSTANT)
+      rt.add(c, 1.0f, out);
+    });
+    const auto got = host(out);
+    size_t bad = 0;
+    for (size_t k = 0; k < ws; ++k) bad += got[k] != values[k] + 1.0f;
+    CHECK(bad == 0);
+  }
+  rt.set_graph_mode(false);
+}
+
+// sqe = (prediction - target)^2 elementwise (runtime.cpp:843-848), with
+// the executor's broadcasting and in place.
+void sqe(hip::Runtime &rt) {
+  Tensor p({2, 3}), t({2, 3}), row({3}), o({2, 3}), ob({2, 3});
+  fill(p, {1, -2, 3.5f, 0, 10, -7});
+  fill(t, {4, -2, 1, 0.25f, -10, 7});
+  fill(row, {1, 2, 3});
+  run(rt, [&] {
+    rt.sqe(p, t, o);
+    rt.sqe(p, row, ob);
+    rt.sqe(p, t, p); // in place: destination is the prediction
+  });
+  expect(o, {9, 0, 6.25f, 0.0625f, 400, 196});
+  expect(ob, {0, 16, 0.25f, 1, 64, 100});
+  expect(p, {9, 0, 6.25f, 0.0625f, 400, 196});
+  // a larger random case against sub-then-square on the host
+  Tensor x({6144, 384}), y({6144, 384}), z({6144, 384});
+  const auto xv = random_values(x.numel(), 31), yv = random_values(y.numel(), 32);
+  x.set(xv);
+  y.set(yv);
+  run(rt, [&] { rt.sqe(x, y, z); });
+  const auto got = host(z);
+  size_t bad = 0;
+  for (size_t i = 0; i < got.size(); ++i) {
+    const float d = xv[i] - yv[i];
+    bad += std::fabs(got[i] - d * d) > 1e-5f + 1e-4f * d * d;
+  }
+  CHECK(bad == 0);
+}
+
 void memory_pool_reuse(hip::Runtime &) {
   const auto before = hip::memory_stats();
   for (int i = 0; i < 10; ++i) {
@@ -640,6 +703,9 @@ int main(int argc, char **argv) {
     harness::run("in_place_and_split_merge", [&] { in_place_and_split_merge(rt); });
     harness::run("batched_matmul_layouts", [&] { batched_matmul_layouts(rt); });
     harness::run("graph_mode", [&] { graph_mode(rt); });
+    harness::run("graph_mode_scratch_is_not_reused_within_a_capture",
+                 [&] { graph_mode_scratch_is_not_reused_within_a_capture(rt); });
+    harness::run("sqe", [&] { sqe(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }

@@ -232,6 +232,28 @@ def test_forward_copies_change_no_bit():
         prog.close()
 
 
+def test_forward_copies_change_no_bit_at_the_benchmark_shapes():
+    # batch 32 x T 192 x d 384 with the 2048-entry vocabulary: the vocab
+    # projection [6144, 2048] x K 384 takes 128x128 tiles, transposed-B on
+    # the copies; one block keeps the oracle-free check cheap
+    prog = GptProgram(2048, 192, 384, 6, 1, 32)
+    try:
+        runs = []
+        for mode in (0, 1):
+            assert prog.set_forward_copies(mode) == bool(mode)
+            prog.init_params(seed=11, std=0.02)
+            prog.set_optimizer(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+            prog.random_batch(seed=12)
+            for _ in range(2):
+                prog.train_step(1.0 / 6144, 1.0)
+            prog.synchronize()
+            runs.append((prog.losses(), prog.get_grads(), prog.get_params()))
+        for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
+            assert np.array_equal(got, want), what
+    finally:
+        prog.close()
+
+
 def read_archive(path):
     """name -> bytes of a checkpoint archive file (u32 name length, name,
     u32 blob length, blob)*."""

@@ -145,6 +145,43 @@ def test_transpose_multi(g):
         np.testing.assert_array_equal(got[do:do + r * c].reshape(c, r), want)
 
 
+def _transpose_jobs(shapes):
+    offs, off = [], 0
+    for r, c in shapes:
+        offs.append(off)
+        off += (r * c + 63) // 64 * 64
+    jobs = np.zeros(len(shapes), JOB)
+    tiles = 0
+    for i, ((r, c), o) in enumerate(zip(shapes, offs)):
+        jobs[i] = (o, o, r, c, tiles, 0)
+        tiles += ((r + 63) // 64) * ((c + 63) // 64)
+    return jobs, offs, off, tiles
+
+
+def test_transpose_multi_extra_tiles_and_inconsistent_tables(g):
+    # blocks past the last job's tiles write nothing; a table whose
+    # first_tile values descend makes the whole launch a no-op
+    shapes = [(100, 70), (64, 64), (3, 200)]
+    jobs, offs, n, tiles = _transpose_jobs(shapes)
+    src = O.normal((n,), 32)
+    sentinel = np.float32(-12345.0)
+    out = g.dev(np.full(n + 4096, sentinel, np.float32))
+    dev_jobs = torch.from_numpy(jobs.view(np.uint8).copy()).to("cuda")
+    g.call("tlh_transpose_multi", g.dev(src), out, dev_jobs, len(shapes), tiles + 37)
+    got = g.host(out)
+    written = np.zeros(got.size, bool)
+    for (r, c), o in zip(shapes, offs):
+        np.testing.assert_array_equal(got[o:o + r * c].reshape(c, r), src[o:o + r * c].reshape(r, c).T)
+        written[o:o + r * c] = True
+    assert np.all(got[~written] == sentinel)
+    bad = jobs.copy()
+    bad["first_tile"][1], bad["first_tile"][2] = bad["first_tile"][2], bad["first_tile"][1]
+    out2 = g.dev(np.full(n, sentinel, np.float32))
+    dev_bad = torch.from_numpy(bad.view(np.uint8).copy()).to("cuda")
+    g.call("tlh_transpose_multi", g.dev(src), out2, dev_bad, len(shapes), tiles)
+    assert np.all(g.host(out2) == sentinel)
+
+
 # ---------------------------------------------------------------------------
 # matmul
 # ---------------------------------------------------------------------------
@@ -409,6 +446,29 @@ def test_gemm_tail_split_gelu_epilogues(g):
     assert_rel(out.reshape(M, N), O.unary("gelu", pre), 1e-3, "gelu")
     out, _ = gemm(g, a, b, epi=EPI_GELU_BWD, aux=pre)
     assert_rel(out.reshape(M, N), O.matmul(a, b) * O.unary("gelu_derivative", pre), 1e-3, "gelu'")
+
+
+@pytest.mark.parametrize("N", [4096, 1024])
+def test_gemm_d1024_shapes(g, N):
+    # The d=1024 products of the scaled configuration, [8192,1024].[1024,N],
+    # N = 4096 (FFN up) and 1024 (attention projections), through the same
+    # call the benchmark times (tlh_gemm, planner's choice, no workspace).
+    # Oracle-free checks against float64 on the host: 96 sampled rows in
+    # full, and every column's sum over all 8192 rows, which equals
+    # (1^T A) B and so covers every output row.
+    M, K = 8192, 1024
+    a = O.normal((M, K), 170, 0, 0.02)
+    b = O.normal((K, N), 171, 0, 0.02)
+    out, _ = gemm(g, a, b, split=False)
+    out = out.reshape(M, N)
+    rows = np.sort(np.concatenate([[0, 63, 64, M - 1], O.uniform_u32((92,), 172, M)]))
+    ref = a[rows].astype(np.float64) @ b.astype(np.float64)
+    assert_rel(out[rows], ref, 1e-3, "sampled rows")
+    col = a.astype(np.float64).sum(axis=0) @ b.astype(np.float64)
+    got = out.astype(np.float64).sum(axis=0)
+    # |sum| of 8192 terms of size ~|ref| cancels; bound by the summed magnitudes
+    scale = np.abs(out.astype(np.float64)).sum(axis=0)
+    assert np.all(np.abs(got - col) <= 1e-4 * scale), float(np.max(np.abs(got - col) / scale))
 
 
 def test_gemm_bias_residual_beta(g):
@@ -700,7 +760,11 @@ def test_softmax_stability_kat(g):
     assert_close(g.host(out), O.softmax(x.reshape(4, 3)))
 
 
-@pytest.mark.parametrize("rows,cols", [(36864, 192), (50, 77)])
+# cols 2048 / 1024 / 512 / 192 run the register kernels for 8 / 4 / 2 / 1
+# float4 per lane and 77 the looped kernel; (6144, 2048) is the row-op
+# configuration the benchmark times
+@pytest.mark.parametrize("rows,cols", [(6144, 2048), (6144, 1024), (6144, 512), (36864, 192),
+                                       (50, 77)])
 def test_softmax_backward(g, rows, cols):
     y = O.softmax(O.normal((rows, cols), 53, 0, 2))
     gr = O.normal((rows, cols), 54)
