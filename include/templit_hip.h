@@ -228,6 +228,26 @@ int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, uint32_t
                   const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
                   float *workspace, size_t workspace_elems, void *stream);
 
+/* Allocation-free form of tlh_matmul_ws. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Takes tlh_matmul's arguments; the K-chunk partials live in a
+ * library-owned device array of TLH_NOALLOC_SCRATCH_FLOATS floats (32 MiB)
+ * that each GPU holds from tlh_init (or the first call on that device)
+ * until the process ends. Runs the plan and gives the results of
+ * tlh_matmul_ws with tlh_matmul_workspace_size's workspace, bit for bit.
+ * Returns hipErrorInvalidValue, launching nothing, when that size exceeds
+ * TLH_NOALLOC_SCRATCH_FLOATS (use tlh_matmul_ws then). Every call on one GPU
+ * shares the array: calls on one stream are ordered, calls that overlap on
+ * one GPU (other streams, other threads) race. Calls no allocator. */
+#define TLH_NOALLOC_SCRATCH_FLOATS (8u * 1024u * 1024u)
+int tlh_matmul_noalloc(const float *a, const float *b, float *c, uint32_t M, uint32_t K,
+                       uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs,
+                       uint32_t b_cs, uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+                       const uint32_t *batch_shape, const uint32_t *batch_stride_a,
+                       const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
+                       void *stream);
+
 /* Fused GEMM used by the program layer (no reference counterpart; it fuses
  * EXPR_LINEAR = mult + in-place bias add (execute.h:241-252), the GELU that
  * follows, the residual add, and MULT_LHS/RHS_DERIVATIVE's transposes

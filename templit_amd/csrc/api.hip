@@ -7,6 +7,7 @@
 // The host runtime (hip::Runtime, Storage<hip::HIP,T>) reaches HIP only
 // through these functions, so it builds with any C++20 compiler.
 #include "common.h"
+#include "gemm.h"
 
 #include <rocprofiler-sdk-roctx/roctx.h>
 
@@ -81,6 +82,8 @@ TLH_API int tlh_init(int device) {
     hipError_t e = hipGetDeviceCount(&count);
     if (e == hipSuccess && (device < 0 || device >= count)) e = hipErrorInvalidDevice;
     if (e == hipSuccess) e = hipSetDevice(device);
+    // the allocation-free entry point's scratch address on this device
+    if (e == hipSuccess) e = hipError_t(tlh::noalloc_scratch(nullptr));
     if (e == hipSuccess) g_device = device;
     g_init_status = int(e);
   });

@@ -66,4 +66,9 @@ size_t gemm_workspace_elems(const GemmDesc &d);
 // Chooses the split count gemm_launch would use for `d` (1 = none).
 int gemm_choose_splits(const GemmDesc &d);
 
+// Device address of the current GPU's copy of the allocation-free entry
+// point's scratch array (TLH_NOALLOC_SCRATCH_FLOATS floats), resolved with
+// hipGetSymbolAddress on the first call per device. Returns hipError_t.
+int noalloc_scratch(float **out);
+
 } // namespace tlh

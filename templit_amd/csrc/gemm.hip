@@ -19,6 +19,7 @@
 #include "gemm.h"
 
 #include <algorithm>
+#include <mutex>
 #include <numeric>
 
 namespace tlh {
@@ -1251,4 +1252,60 @@ TLH_API int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, 
   }
   return tlh::gemm_launch(d, stream);
 }
+TLH_API int tlh_matmul_noalloc(const float *a, const float *b, float *c, uint32_t M,
+                               uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
+                               uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
+                               uint32_t batch_ndim, const uint32_t *batch_shape,
+                               const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                               const uint32_t *batch_stride_c, void *stream) {
+  tlh::GemmDesc d;
+  bool skip = false;
+  int st = matmul_desc(TLH_MATMUL_ARGS, d, skip);
+  if (st || skip) return st;
+  const size_t need = tlh::gemm_workspace_elems(d);
+  if (need > TLH_NOALLOC_SCRATCH_FLOATS) return int(hipErrorInvalidValue);
+  if (need) {
+    float *ws = nullptr;
+    if ((st = tlh::noalloc_scratch(&ws))) return st;
+    d.workspace = ws;
+    d.workspace_elems = need;
+  }
+  return tlh::gemm_launch(d, stream);
+}
 #undef TLH_MATMUL_ARGS
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point
+// ---------------------------------------------------------------------------
+// K-chunk partials of tlh_matmul_noalloc. Each GPU the library runs on holds
+// its own copy from module load until the process ends. In host code the
+// name `scratch` is a host-side stand-in, not a device address: kernels get
+// the address hipGetSymbolAddress returns for the current device, resolved
+// once per device and kept in g_scratch_ptr. Every partial plane is written
+// before it is read, so the array needs no clearing between calls.
+static __device__ __align__(256) float scratch[TLH_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxScratchDevices] = {};
+} // namespace
+
+namespace tlh {
+int noalloc_scratch(float **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return int(hipErrorInvalidDevice);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return int(e);
+    if (!p) return int(hipErrorInvalidSymbol);
+    g_scratch_ptr[dev] = static_cast<float *>(p);
+  }
+  if (out) *out = g_scratch_ptr[dev];
+  return 0;
+}
+} // namespace tlh

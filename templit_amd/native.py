@@ -110,6 +110,9 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_matmul_ws": [P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                       c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P, U32P, P, c_size_t,
                       P],
+    "tlh_matmul_noalloc": [P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                           c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P,
+                           U32P, P],
     "tlh_gemm": [POINTER(GemmDesc), P],
     "tlh_gemm_workspace_size": [POINTER(GemmDesc), POINTER(c_size_t)],
     "tlh_gemm_set_plan": [c_int, c_int, c_int, c_int],
