@@ -1,10 +1,13 @@
-// Batch loader over a token span (see model_utils/Dataset.h for the
-// dataset). Same interface and behaviour as the reference's
-// (include/model_utils/loader.h, src/model_utils/loader.cpp:5-43): each
-// sample start is drawn uniformly from [0, size - len] with
-// std::uniform_int_distribution<size_t> over std::mt19937(seed) -- the
-// same standard-library engine and distribution, so one seed gives the
-// reference's batches on the same C++ standard library.
+// Batch loader over a token span (the dataset is model_utils/Dataset.h).
+//
+// A drop-in for the reference's Loader (include/model_utils/loader.h,
+// behaviour of src/model_utils/loader.cpp:5-43). Sample starts are the
+// reference's draws: std::uniform_int_distribution<size_t> over [0, size -
+// len] from std::mt19937(seed), one draw per sample in batch order, so one
+// seed gives the reference's batches on the same C++ standard library.
+// get_batch fills one [batch, sequence] buffer of inputs and its one-token
+// shift of targets, reused across calls (the form the GPT program uploads
+// to the device in one copy each).
 #pragma once
 
 #include <cstddef>
@@ -20,18 +23,21 @@ public:
     std::vector<uint32_t> targets; // inputs shifted by one position
   };
 
-private:
-  std::span<const uint32_t> dataset_;
-  std::mt19937 generator_;
-  Batch batch_;
-
-public:
-  // Throws std::invalid_argument for an empty dataset.
+  // Throws std::invalid_argument for an empty dataset. `dataset` must
+  // outlive the loader.
   explicit Loader(std::span<const uint32_t> dataset, uint32_t seed = 1);
 
   // `len` consecutive tokens from a uniformly drawn start; throws
   // std::invalid_argument if len is 0 or longer than the dataset.
   std::span<const uint32_t> get_sample(size_t len);
-  // batch_size samples of sequence_size + 1 tokens; valid until the next call.
+  // batch_size windows of sequence_size + 1 tokens, split into inputs and
+  // targets; the reference stays valid until the next call.
   const Batch &get_batch(size_t batch_size, size_t sequence_size);
+
+private:
+  size_t draw_start(size_t len);
+
+  std::span<const uint32_t> tokens_;
+  std::mt19937 engine_;
+  Batch out_;
 };

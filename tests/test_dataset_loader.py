@@ -78,3 +78,28 @@ def test_c_abi_loader_errors(tmp_path):
         assert x.size == 16
     finally:
         loader.close()
+
+
+def test_text_decoding_across_read_chunks(tmp_path):
+    # Dataset::load_text reads in 64 KiB chunks: blank lines that straddle a
+    # chunk boundary, a lone newline ending a chunk and runs of three
+    # newlines must decode as in one piece. Expected ids: the text split on
+    # non-overlapping "\n\n" (left to right), pieces joined by the
+    # end-of-sequence id 256, every other byte its own value.
+    chunk = 64 * 1024
+    text = bytearray(b"x" * (3 * chunk + 100))
+    text[chunk - 1:chunk + 1] = b"\n\n"            # a blank line across the boundary
+    text[2 * chunk - 1] = ord("\n")                 # a lone newline ending a chunk
+    text[2 * chunk + 10:2 * chunk + 13] = b"\n\n\n"  # three newlines
+    text[3 * chunk - 2:3 * chunk + 1] = b"\n\n\n"    # three across the boundary
+    text[-1:] = b"\n"
+    src, out = tmp_path / "t.txt", tmp_path / "t.tokens"
+    src.write_bytes(bytes(text))
+    subprocess.run([str(ROOT / "tests" / "cpp" / "bin" / "test_loader"), "--text-to-tokens",
+                    str(src), str(out)], check=True)
+    expect = []
+    for i, piece in enumerate(bytes(text).split(b"\n\n")):
+        if i:
+            expect.append(256)
+        expect.extend(piece)
+    np.testing.assert_array_equal(np.fromfile(out, np.uint32), np.array(expect, np.uint32))
