@@ -374,7 +374,68 @@ def cpu_baseline(sample_batch: int, steps: int) -> dict:
             "kind": "port",
             "sample": f"{steps} oracle training steps of the same model at batch "
                       f"{sample_batch} ({rows} tokens/step, {dt:.1f} s), single thread",
-            "kernel_configs": cpu_kernel_configs()}
+            **host_cpu(),
+            "kernel_configs": cpu_kernel_configs(),
+            "reference_cpu_runtime": reference_cpu_kernels()}
+
+
+def host_cpu() -> dict:
+    """CPU model and core counts of the machine the baseline ran on."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"cpu_model": model, "nproc": usable, "cpu_count": os.cpu_count()}
+
+
+def reference_cpu_kernels() -> dict | None:
+    """The reference's own CPU runtime (src/CPU/cpu.cpp, compiled from its
+    sources into oracle/_ref/libref_cpu.so at -O2, one thread) on the
+    configurations it can run: matmul + bias (config 1, mult then the
+    broadcast add) and the [6144,2048] softmax. Times include copying the
+    operands into and out of its tensors (a few MB, well under 1 %)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import numpy as np
+    import oracle_lib as O
+
+    if not O.ref_available():
+        return None
+    r = O.ref()
+    M, K, N = C1
+    a, b, bias = O.normal((M, K), 1, 0, 0.02), O.normal((K, N), 2, 0, 0.02), O.normal((1, N), 3)
+    c, out = np.empty((M, N), np.float32), np.empty((M, N), np.float32)
+    x, y = O.normal((R2, V2), 9), np.empty((R2, V2), np.float32)
+
+    def best_of(fn, n=3):
+        times = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return min(times)
+
+    def mult_add():
+        assert r.ref_mult(O.p(a), O.p(b), O.p(c), M, K, N) == 0
+        assert r.ref_binary(0, O.p(c), M, N, O.p(bias), 1, N, O.p(out)) == 0
+
+    mm = best_of(mult_add)
+    sm = best_of(lambda: r.ref_softmax(O.p(x), O.p(y), R2, V2))
+    res = {"kind": "reference", "cores": 1, "build": "clang++ -O2 (the reference's default)",
+           "matmul_bias_768x384x1536": {"s": round(mm, 4),
+                                        "gflops": round((2.0 * M * N * K + M * N) / mm / 1e9, 2)},
+           "softmax_6144x2048": {"s": round(sm, 4),
+                                 "gb_s": round(ROW_OP_BYTES["softmax_fwd"] / sm / 1e9, 2)},
+           "timing": "best of 3 calls"}
+    log(f"[bench] reference CPU runtime: {json.dumps(res)}")
+    return res
 
 
 def cpu_kernel_configs() -> dict:

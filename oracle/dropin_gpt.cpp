@@ -364,13 +364,51 @@ int run(bool cpu_only, bool layout) {
   return g_failures ? 1 : 0;
 }
 
-// Usage: dropin_gpt [--cpu-only | --archive-layout]
+// The same comparison at the benchmark model's sizes (BenchDims: V 2048,
+// T 192, d 384, 6 heads, 4 blocks, batch 2), where hip::Runtime's products
+// take the large-shape plans (128x128 tiles for the vocabulary projection,
+// split-K and tail splits with pool scratch, the tall column sums).
+int run_bench_shapes() {
+  using D = BenchDims;
+  const uint32_t seed = 1;
+  const float max_norm = 1.0f;
+  std::vector<uint32_t> tokens(D::batch * D::seq), targets(D::batch * D::seq);
+  uint64_t s = 7;
+  for (auto &t : tokens) t = uint32_t(splitmix(s) % D::vocab);
+  for (auto &t : targets) t = uint32_t(splitmix(s) % D::vocab);
+  std::printf("reference nn::GPT<V=%u, T=%u, D=%u, H=%u> (4 blocks), batch %u, clip %.1f, AdamW, "
+              "%d steps\n",
+              D::vocab, D::seq, D::dim, D::heads, D::batch, max_norm, kSteps);
+  orc::Runtime cpu;
+  const Outcome ref = train_oracle_bench(cpu, tokens, targets, seed, max_norm);
+  std::printf("oracle runtime: loss %.6f -> %.6f\n", ref.losses[0][0], ref.losses[1][0]);
+  hip::init(0);
+  {
+    hip::Runtime gpu;
+    const Outcome eager = train_hip_bench(gpu, tokens, targets, seed, max_norm);
+    compare("hip::Runtime (eager) vs oracle runtime, benchmark shapes", eager, ref, 1e-4, 1e-3);
+    gpu.set_graph_mode(true);
+    const Outcome graph = train_hip_bench(gpu, tokens, targets, seed, max_norm);
+    compare("hip::Runtime (graph mode) vs oracle runtime, benchmark shapes", graph, ref, 1e-4,
+            1e-3, false);
+    const auto st = gpu.graph_stats();
+    std::printf("graph mode: %zu recordings, %zu instantiations, %zu in-place updates\n",
+                st.captures, st.instantiations, st.updates);
+  }
+  hip::shutdown();
+  std::printf("%s\n", g_failures ? "DROP-IN PARITY FAILED" : "drop-in parity ok");
+  return g_failures ? 1 : 0;
+}
+
+// Usage: dropin_gpt [--cpu-only | --archive-layout | --bench-shapes]
 //   --cpu-only: only the oracle runtime and its anchor (no GPU needed).
 //   --archive-layout: print the reference checkpoint layout of this GPT as
 //     JSON after "ARCHIVE LAYOUT" (no GPU needed).
+//   --bench-shapes: hip::Runtime vs the oracle runtime at BenchDims.
 int main(int argc, char **argv) {
   std::setvbuf(stdout, nullptr, _IOLBF, 0);
   try {
+    if (argc > 1 && std::strcmp(argv[1], "--bench-shapes") == 0) return run_bench_shapes();
     const bool layout = argc > 1 && std::strcmp(argv[1], "--archive-layout") == 0;
     return run(layout || (argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0), layout);
   } catch (const std::exception &e) {

@@ -68,17 +68,18 @@ private:
   Optimiser::AdamW<T> inner_;
 };
 
-template <typename Mat, typename Run>
+template <typename Mat, typename Dims, typename Run>
 Outcome train(Run &rt, const std::vector<uint32_t> &tokens, const std::vector<uint32_t> &targets,
               uint32_t seed, float max_norm) {
   using IndexMat = typename Mat::template rebind<uint32_t>;
+  constexpr uint32_t kBatch = Dims::batch, kSeq = Dims::seq;
   IndexMat in_v({kBatch, kSeq}), tg_v({kBatch, kSeq});
   in_v.set(std::span<const uint32_t>(tokens));
   tg_v.set(std::span<const uint32_t>(targets));
   expr::tensor::Tensor input(std::move(in_v));
   expr::tensor::Tensor target(std::move(tg_v));
   std::mt19937 gen(seed);
-  nn::GPT<Mat, kVocab, kSeq, kDim, kHeads> model(kBatch, kSeq, gen);
+  nn::GPT<Mat, Dims::vocab, Dims::seq, Dims::dim, Dims::heads> model(kBatch, kSeq, gen);
   auto graph = model(input);
   auto loss = expr::loss::cross_entropy(graph, target);
   using Opt = RecordingAdamW<Mat>;

@@ -7,6 +7,6 @@
 namespace dropin {
 Outcome train_hip(hip::Runtime &rt, const std::vector<uint32_t> &tokens,
                   const std::vector<uint32_t> &targets, uint32_t seed, float max_norm) {
-  return train<RTensor<hip::HIP, float>>(rt, tokens, targets, seed, max_norm);
+  return train<RTensor<hip::HIP, float>, SmallDims>(rt, tokens, targets, seed, max_norm);
 }
 } // namespace dropin

@@ -41,3 +41,13 @@ def test_reference_executor_on_hip_runtime():
     proc = _run()
     assert proc.returncode == 0, proc.stdout
     assert "drop-in parity ok" in proc.stdout
+
+
+@needs_bin
+@pytest.mark.gpu
+def test_reference_executor_on_hip_runtime_at_the_benchmark_shapes():
+    # V 2048, T 192, d 384, 6 heads, 4 blocks at batch 2: the large-shape
+    # product plans, split-K / tail-split scratch and tall column sums
+    proc = _run("--bench-shapes")
+    assert proc.returncode == 0, proc.stdout
+    assert "drop-in parity ok" in proc.stdout
