@@ -163,6 +163,38 @@ def build_cpp_tests() -> list[Path]:
     return out
 
 
+# Host AddressSanitizer + UndefinedBehaviorSanitizer builds of the C++ test
+# programs and the host sources they exercise (archive, dataset, loader, the
+# runtime's no-device path), as the reference builds by default
+# (CMakeLists.txt:8,18-27). g++ only: no device code is built with them.
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+             "-fno-omit-frame-pointer", "-g"]
+SAN_SOURCES = {
+    "test_archive": ["archive.cpp"],
+    "test_loader": ["dataset.cpp", "loader.cpp"],
+    "test_hip_runtime": ["runtime.cpp", "hip_context.cpp", "archive.cpp", "dataset.cpp",
+                         "loader.cpp"],
+}
+
+
+def build_sanitized_tests() -> list[Path]:
+    tdir = ROOT / "tests" / "cpp"
+    bindir = tdir / "bin" / "san"
+    bindir.mkdir(parents=True, exist_ok=True)
+    flags = HOST_FLAGS + SAN_FLAGS + [f"-I{tdir}"]
+    out = []
+    for name, sources in SAN_SOURCES.items():
+        objs = [_compile(tdir / f"{name}.cpp", flags, "g++")]
+        objs += [_compile(CSRC / src, flags, "g++") for src in sources]
+        exe = bindir / name
+        tmp = exe.with_suffix(".tmp")
+        _run(["g++", *SAN_FLAGS, "-o", str(tmp), *map(str, objs), f"-L{PKG}", "-ltemplit_hip",
+              "-Wl,-rpath,$ORIGIN/../../../../templit_amd"])
+        tmp.replace(exe)
+        out.append(exe)
+    return out
+
+
 def clean_stale_objects() -> None:
     if not BUILD.exists():
         return
@@ -182,6 +214,7 @@ def build_all() -> None:
     build_runtime(lib)
     build_gpt(lib)
     build_cpp_tests()
+    build_sanitized_tests()
     clean_stale_objects()
 
 

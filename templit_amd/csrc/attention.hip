@@ -36,6 +36,13 @@ constexpr int LDP = HD + 4;  // padded LDS row (floats)
 constexpr int KB = 64;       // rows per streamed LDS tile
 constexpr int WQ = 32;       // rows per wave
 constexpr int BQ = 2 * WQ;   // rows per block (two row tiles x two halves of the stream)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 2^x on the hardware unit (v_exp_f32): 2^-inf = 0, results below the
+// normal range flush to 0. Softmax and its backward evaluate
+// exp(s*scale - m) as 2^(s*scale*log2(e) - m*log2(e)).
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct Dims {
   uint32_t B, H, T;
@@ -175,7 +182,10 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+  // the running max m_run is kept in base-2 units (scores times
+  // scale*log2(e)), so every exponential is one hardware 2^x
   float m_run = -INFINITY, l_run = 0.f;
+  const float scale2 = scale * kLog2e;
 
   const int q_end = min(int(d.T), q_block + BQ);
   const int k_end = causal ? q_end : int(d.T);
@@ -205,13 +215,15 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
 #pragma unroll
       for (int j = 0; j < 4; ++j) st = mfma(ka[j], qreg[4 * s4 + j], st);
     }
-    // scale, mask, online softmax (per query = r; keys spread over v and h)
+    // scale, mask, online softmax (per query = r; keys spread over v and h);
+    // only tiles on the causal diagonal or past the sequence end need the mask
+    const bool masked = k0 + WQ > int(d.T) || (causal && k0 + WQ - 1 > q0);
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = k0 + key_of(i, hh);
-      float sv = st[i] * scale;
-      if (key >= int(d.T) || (causal && key > my_q)) sv = -INFINITY;
+      float sv = st[i] * scale2;
+      if (masked && (key >= int(d.T) || (causal && key > my_q))) sv = -INFINITY;
       st[i] = sv;
       mx = fmaxf(mx, sv);
     }
@@ -221,12 +233,12 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
     float ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = expf(st[i] - m_use);
+      const float p = exp2_fast(st[i] - m_use);
       st[i] = p;
       ps += p;
     }
     ps += __shfl_xor(ps, 32, 64);
-    const float alpha = expf(m_run - m_use);
+    const float alpha = exp2_fast(m_run - m_use);
     l_run = l_run * alpha + ps;
     m_run = m_new;
 #pragma unroll
@@ -260,7 +272,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
       const float m1 = buf[2 * 16 * 64 + r], l1 = buf[2 * 16 * 64 + WQ + r];
       const float m = fmaxf(m_run, m1);
       const float mu = (m == -INFINITY) ? 0.f : m;
-      const float a0 = expf(m_run - mu), a1 = expf(m1 - mu);
+      const float a0 = exp2_fast(m_run - mu), a1 = exp2_fast(m1 - mu);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -273,7 +285,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
   // epilogue: O = O / l ; lse = m + log(l)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
   if (active && half == 0 && hh == 0 && my_q < int(d.T))
-    lse[(size_t(b) * d.H + h) * d.T + my_q] = m_run + logf(l_run);
+    lse[(size_t(b) * d.H + h) * d.T + my_q] = m_run * kLn2 + logf(l_run);
   store_rows_via_lds(smem, oacc, inv_l, o, d, b, h, q0, o_merged, lane, wave,
                      active && half == 0);
 }
@@ -318,6 +330,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
 
   const size_t lse_base = (size_t(b) * d.H + h) * d.T;
   const int q_start = causal ? (k_block / KB) * KB : 0;
+  const float scale2 = scale * kLog2e;
   // Q/dO tile (and its lse, delta) qt0+KB is fetched while qt0 is in use.
   TileRegs qpre, dopre;
   float lse_pre = 0.f, delta_pre = 0.f;
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
     put_tile(Qs, qpre);
     put_tile(dOs, dopre);
     if (threadIdx.x < KB) {
-      lse_s[threadIdx.x] = lse_pre;
+      lse_s[threadIdx.x] = lse_pre * kLog2e; // base-2 units
       delta_s[threadIdx.x] = delta_pre;
     }
     __syncthreads();
@@ -364,13 +377,16 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kv_kernel(
         dp = mfma(da[j], vreg[4 * s4 + j], dp);
       }
     }
-    // P = exp(S*scale - lse[q]) masked; dS = P * (dP - delta[q])
+    // P = exp(S*scale - lse[q]) masked; dS = P * (dP - delta[q]); only
+    // tiles on the causal diagonal or past the sequence end need the mask
+    const bool masked = qh0 + WQ > int(d.T) || key0 + WQ > int(d.T) ||
+                        (causal && key0 + WQ - 1 > qh0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int ql = key_of(i, hh);
       const int qq = qh0 + ql;
-      float p = expf(sp[i] * scale - lse_h[ql]);
-      if (qq >= int(d.T) || my_key >= int(d.T) || (causal && my_key > qq)) p = 0.f;
+      float p = exp2_fast(sp[i] * scale2 - lse_h[ql]);
+      if (masked && (qq >= int(d.T) || my_key >= int(d.T) || (causal && my_key > qq))) p = 0.f;
       sp[i] = p;
       dp[i] = p * (dp[i] - delta_h[ql]);
     }
@@ -430,7 +446,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
   const size_t do_off = row_off(d, b, h, qvalid ? my_q : 0, o_merged) + 32 * hh;
   load_row_half(doreg, dout + do_off, qvalid);
   const size_t lse_base = (size_t(b) * d.H + h) * d.T;
-  const float my_lse = qvalid ? lse[lse_base + my_q] : 0.f;
+  const float my_lse2 = qvalid ? lse[lse_base + my_q] * kLog2e : 0.f; // base-2 units
+  const float scale2 = scale * kLog2e;
   // delta = dO . O for this query (the two lane halves hold 32 dims each);
   // stored for the dK/dV kernel, which runs next
   float my_delta = 0.f;
@@ -483,11 +500,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
         dpt = mfma(va[j], doreg[4 * s4 + j], dpt);
       }
     }
+    const bool masked = k0 + WQ > int(d.T) || (causal && k0 + WQ - 1 > q0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = k0 + key_of(i, hh);
-      float p = expf(st[i] * scale - my_lse);
-      if (!qvalid || key >= int(d.T) || (causal && key > my_q)) p = 0.f;
+      float p = exp2_fast(st[i] * scale2 - my_lse2);
+      if (!qvalid || (masked && (key >= int(d.T) || (causal && key > my_q)))) p = 0.f;
       dpt[i] = p * (dpt[i] - my_delta);
     }
     // dQ^T[dim][q] += K^T[dim][key] . dS^T[key][q]

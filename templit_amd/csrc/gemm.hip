@@ -271,6 +271,104 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
   }
 }
 
+
+// Global -> register fetch of one K tile of both operands (A_CHUNKS and
+// B_CHUNKS float4 per thread), zero-filled outside the matrix unless FULL.
+// Summed batch entries (seg_k > 0): a K tile never straddles a segment.
+template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL>
+__device__ inline void fetch_operands(const GemmParams &p, const float *A, const float *B, int m0,
+                                      int n0, int k0, int k_end, f4 (&ra)[BM * BK / 1024],
+                                      f4 (&rb)[BN * BK / 1024]) {
+  constexpr int A_CHUNKS = BM * BK / 1024, B_CHUNKS = BN * BK / 1024;
+  const int tid = threadIdx.x;
+  const float *As = A, *Bs = B;
+  int kofs = 0; // global k minus the segment-local k
+  if (p.seg_k > 0) {
+    const int sg = k0 / p.seg_k;
+    kofs = sg * p.seg_k;
+    As += size_t(sg) * p.seg_a;
+    Bs += size_t(sg) * p.seg_b;
+  }
+#pragma unroll
+  for (int i = 0; i < A_CHUNKS; ++i) {
+    const int c = tid + i * 256;
+    int row, col; // in stored layout
+    if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+    else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
+    const int grow = TA ? (k0 + row) : (m0 + row);
+    const int gcol = TA ? (m0 + col) : (k0 + col);
+    const int row_lim = TA ? k_end : p.M;
+    const int col_lim = TA ? p.M : k_end;
+    const float *src = As + size_t(TA ? grow - kofs : grow) * p.lda + (TA ? gcol : gcol - kofs);
+    if constexpr (FULL) {
+      ra[i] = *reinterpret_cast<const f4 *>(src);
+    } else {
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (grow < row_lim) {
+        if (VEC && gcol + 3 < col_lim) {
+          v = *reinterpret_cast<const f4 *>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (gcol + j < col_lim) v[j] = src[j];
+        }
+      }
+      ra[i] = v;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < B_CHUNKS; ++i) {
+    const int c = tid + i * 256;
+    int row, col;
+    if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+    else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
+    const int grow = TB ? (n0 + row) : (k0 + row);
+    const int gcol = TB ? (k0 + col) : (n0 + col);
+    const int row_lim = TB ? p.N : k_end;
+    const int col_lim = TB ? k_end : p.N;
+    const float *src = Bs + size_t(TB ? grow : grow - kofs) * p.ldb + (TB ? gcol - kofs : gcol);
+    if constexpr (FULL) {
+      rb[i] = *reinterpret_cast<const f4 *>(src);
+    } else {
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (grow < row_lim) {
+        if (VEC && gcol + 3 < col_lim) {
+          v = *reinterpret_cast<const f4 *>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (gcol + j < col_lim) v[j] = src[j];
+        }
+      }
+      rb[i] = v;
+    }
+  }
+}
+
+// Register -> LDS store of the fetched K tile: K-contiguous tiles as [rows]
+// [BK + pad], row-contiguous tiles as [BK][rows + pad].
+template <int BM, int BN, int BK, int A_LD, int B_LD, bool TA, bool TB>
+__device__ inline void stage_operands(float *as, float *bs, const f4 (&ra)[BM * BK / 1024],
+                                      const f4 (&rb)[BN * BK / 1024]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < BM * BK / 1024; ++i) {
+    const int c = tid + i * 256;
+    int row, col;
+    if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+    else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
+    *reinterpret_cast<f4 *>(as + row * A_LD + col) = ra[i];
+  }
+#pragma unroll
+  for (int i = 0; i < BN * BK / 1024; ++i) {
+    const int c = tid + i * 256;
+    int row, col;
+    if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
+    else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
+    *reinterpret_cast<f4 *>(bs + row * B_LD + col) = rb[i];
+  }
+}
+
 // FULL: M, N are multiples of the tile, the K range of every block is a
 // multiple of BK and the operands are float4-aligned: no bounds checks.
 template <int BM, int BN, int WM, int WN, int BK, bool TA, bool TB, bool VEC, bool FULL>
@@ -308,92 +406,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 
   // ---- global -> register prefetch ----------------------------------------
   f4 ra[A_CHUNKS], rb[B_CHUNKS];
-
   auto load_tile = [&](int k0) {
-    // K tiles never straddle a segment (seg_k is a multiple of the K tile)
-    const float *As = A, *Bs = B;
-    int kofs = 0; // global k minus the segment-local k
-    if (p.seg_k > 0) {
-      const int sg = k0 / p.seg_k;
-      kofs = sg * p.seg_k;
-      As += size_t(sg) * p.seg_a;
-      Bs += size_t(sg) * p.seg_b;
-    }
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      int row, col; // in stored layout
-      if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
-      else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
-      const int grow = TA ? (k0 + row) : (m0 + row);
-      const int gcol = TA ? (m0 + col) : (k0 + col);
-      const int row_lim = TA ? k_end : p.M;
-      const int col_lim = TA ? p.M : k_end;
-      const float *src = As + size_t(TA ? grow - kofs : grow) * p.lda + (TA ? gcol : gcol - kofs);
-      if constexpr (FULL) {
-        ra[i] = *reinterpret_cast<const f4 *>(src);
-      } else {
-        f4 v = {0.f, 0.f, 0.f, 0.f};
-        if (grow < row_lim) {
-          if (VEC && gcol + 3 < col_lim) {
-            v = *reinterpret_cast<const f4 *>(src);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (gcol + j < col_lim) v[j] = src[j];
-          }
-        }
-        ra[i] = v;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      int row, col;
-      if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
-      else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
-      const int grow = TB ? (n0 + row) : (k0 + row);
-      const int gcol = TB ? (k0 + col) : (n0 + col);
-      const int row_lim = TB ? p.N : k_end;
-      const int col_lim = TB ? k_end : p.N;
-      const float *src = Bs + size_t(TB ? grow : grow - kofs) * p.ldb + (TB ? gcol - kofs : gcol);
-      if constexpr (FULL) {
-        rb[i] = *reinterpret_cast<const f4 *>(src);
-      } else {
-        f4 v = {0.f, 0.f, 0.f, 0.f};
-        if (grow < row_lim) {
-          if (VEC && gcol + 3 < col_lim) {
-            v = *reinterpret_cast<const f4 *>(src);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (gcol + j < col_lim) v[j] = src[j];
-          }
-        }
-        rb[i] = v;
-      }
-    }
+    fetch_operands<BM, BN, BK, TA, TB, VEC, FULL>(p, A, B, m0, n0, k0, k_end, ra, rb);
   };
-
   auto store_tile = [&](int buf) {
     float *as = smem + buf * (A_TILE + B_TILE);
-    float *bs = as + A_TILE;
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      int row, col;
-      if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
-      else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
-      *reinterpret_cast<f4 *>(as + row * A_LD + col) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      int row, col;
-      if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
-      else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
-      *reinterpret_cast<f4 *>(bs + row * B_LD + col) = rb[i];
-    }
+    stage_operands<BM, BN, BK, A_LD, B_LD, TA, TB>(as, as + A_TILE, ra, rb);
   };
 
   f16x acc[TM][TN];
@@ -485,6 +503,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   if (do_bias) bias_grad_store<BN>(p, ctx, smem, bsum, FULL);
   store_acc<BN, TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
 }
+
 
 // ---- one-row products (M = 1): GEMV ------------------------------------------
 // y = x . B with x [1, K] and B [K, N] row-major: memory-bound on B, and a
@@ -736,6 +755,7 @@ int g_xcd_rects = 1;
 int g_gemv = 1;
 // float4 split-K reduce over a (plane, entry) grid (see gemm_splitk_reduce4)
 int g_reduce4 = 1;
+
 
 // The 8-way partition of a tiles_m x tiles_n grid into equal rectangles
 // (1x8, 2x4, 4x2 or 8x1 of them) whose rectangle needs the fewest operand

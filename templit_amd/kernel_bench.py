@@ -24,8 +24,8 @@ from templit_amd.native import GemmDesc, check, load_hip
 
 R, D, F, V = 6144, 384, 1536, 2048
 GEMM_SHAPES = [  # name, M, N, K, trans_a, trans_b, bias gradient
-    ("qkv/o fwd", R, D, D, 0, 0, 0), ("w1 fwd", R, F, D, 0, 0, 0),
-    ("w2 fwd", R, D, F, 0, 0, 0), ("vocab fwd", R, V, D, 0, 0, 0),
+    ("qkv/o fwd", R, D, D, 0, 1, 0), ("w1 fwd", R, F, D, 0, 1, 0),
+    ("w2 fwd", R, D, F, 0, 1, 0), ("vocab fwd", R, V, D, 0, 1, 0),
     ("dX d->d", R, D, D, 0, 1, 0), ("dG d->f", R, F, D, 0, 1, 0),
     ("dN f->d", R, D, F, 0, 1, 0), ("dX vocab", R, D, V, 0, 1, 0),
     ("wgrad dd", D, D, R, 1, 0, 1), ("wgrad fd", F, D, R, 1, 0, 1),
@@ -156,6 +156,8 @@ def run_gemm(b: Bench, iters: int, sweep: bool, only: str | None = None) -> None
         if sweep:
             best_us, best = min(results)
             line += f" | best {best_us:8.1f} us plan {best}"
+            line += "\n    " + " ".join(f"{p_[0]}x{p_[1]}/s{p_[2]}/k{p_[3]}:{u:.1f}"
+                                        for u, p_ in results[1:])
         print(line, flush=True)
 
 

@@ -6,6 +6,7 @@ The oracle is the checker: tests compare the HIP path against it.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from ctypes import POINTER, c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
 from pathlib import Path
@@ -14,8 +15,10 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parents[1]
 ORACLE_DIR = ROOT / "oracle"
-ORACLE_LIB = ORACLE_DIR / "liboracle.so"
-REF_LIB = ORACLE_DIR / "_ref" / "libref_cpu.so"
+# TEMPLIT_ORACLE_LIB / TEMPLIT_REF_CPU_LIB select other builds of the same
+# sources (the sanitizer builds of tests/test_sanitizers.py)
+ORACLE_LIB = Path(os.environ.get("TEMPLIT_ORACLE_LIB", ORACLE_DIR / "liboracle.so"))
+REF_LIB = Path(os.environ.get("TEMPLIT_REF_CPU_LIB", ORACLE_DIR / "_ref" / "libref_cpu.so"))
 
 F32P = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 U32P = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
