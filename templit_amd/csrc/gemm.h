@@ -66,6 +66,10 @@ size_t gemm_workspace_elems(const GemmDesc &d);
 // Chooses the split count gemm_launch would use for `d` (1 = none).
 int gemm_choose_splits(const GemmDesc &d);
 
+// Compute units of the current device (256 when the query fails), cached
+// per device.
+int cu_count();
+
 // Device address of the current GPU's copy of the allocation-free entry
 // point's scratch array (TLH_NOALLOC_SCRATCH_FLOATS floats), resolved with
 // hipGetSymbolAddress on the first call per device. Returns hipError_t.

@@ -27,6 +27,8 @@ namespace {
 
 constexpr int kBK = 32; // largest K tile; split-K chunks are multiples of it
 constexpr int kPad = 4;
+// Row padding of the 16x16 kernels' K-contiguous LDS tiles (see gemm_mfma16_kernel).
+constexpr int kPad16 = 8;
 
 struct GemmParams {
   const float *A;
@@ -64,6 +66,10 @@ struct GemmParams {
   // tail_splits K chunks of tail_k_chunk whose partial tiles go to the
   // workspace ([tail tile][split][BM*BN]) for gemm_tail_reduce. 0 = off.
   int dp_tiles, tail_tiles, tail_splits, tail_k_chunk;
+  // Output rows (C, residual, aux, or the raw partial planes) take float4
+  // access at multiples of 4 columns: 16-byte aligned bases and row
+  // strides, and 4 | remap_d for the head layout (set by the host).
+  int out_vec;
 };
 
 __device__ inline size_t out_index(const GemmParams &p, int m, int n) {
@@ -275,11 +281,11 @@ __device__ inline void store_acc(const GemmParams &p, const BlockCtx &b, const f
 // Global -> register fetch of one K tile of both operands (A_CHUNKS and
 // B_CHUNKS float4 per thread), zero-filled outside the matrix unless FULL.
 // Summed batch entries (seg_k > 0): a K tile never straddles a segment.
-template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL>
+template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL, int NT = 256>
 __device__ inline void fetch_operands(const GemmParams &p, const float *A, const float *B, int m0,
-                                      int n0, int k0, int k_end, f4 (&ra)[BM * BK / 1024],
-                                      f4 (&rb)[BN * BK / 1024]) {
-  constexpr int A_CHUNKS = BM * BK / 1024, B_CHUNKS = BN * BK / 1024;
+                                      int n0, int k0, int k_end, f4 (&ra)[BM * BK / (4 * NT)],
+                                      f4 (&rb)[BN * BK / (4 * NT)]) {
+  constexpr int A_CHUNKS = BM * BK / (4 * NT), B_CHUNKS = BN * BK / (4 * NT);
   const int tid = threadIdx.x;
   const float *As = A, *Bs = B;
   int kofs = 0; // global k minus the segment-local k
@@ -291,7 +297,7 @@ __device__ inline void fetch_operands(const GemmParams &p, const float *A, const
   }
 #pragma unroll
   for (int i = 0; i < A_CHUNKS; ++i) {
-    const int c = tid + i * 256;
+    const int c = tid + i * NT;
     int row, col; // in stored layout
     if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
     else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
@@ -318,7 +324,7 @@ __device__ inline void fetch_operands(const GemmParams &p, const float *A, const
   }
 #pragma unroll
   for (int i = 0; i < B_CHUNKS; ++i) {
-    const int c = tid + i * 256;
+    const int c = tid + i * NT;
     int row, col;
     if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
     else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
@@ -347,21 +353,21 @@ __device__ inline void fetch_operands(const GemmParams &p, const float *A, const
 
 // Register -> LDS store of the fetched K tile: K-contiguous tiles as [rows]
 // [BK + pad], row-contiguous tiles as [BK][rows + pad].
-template <int BM, int BN, int BK, int A_LD, int B_LD, bool TA, bool TB>
-__device__ inline void stage_operands(float *as, float *bs, const f4 (&ra)[BM * BK / 1024],
-                                      const f4 (&rb)[BN * BK / 1024]) {
+template <int BM, int BN, int BK, int A_LD, int B_LD, bool TA, bool TB, int NT = 256>
+__device__ inline void stage_operands(float *as, float *bs, const f4 (&ra)[BM * BK / (4 * NT)],
+                                      const f4 (&rb)[BN * BK / (4 * NT)]) {
   const int tid = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < BM * BK / 1024; ++i) {
-    const int c = tid + i * 256;
+  for (int i = 0; i < BM * BK / (4 * NT); ++i) {
+    const int c = tid + i * NT;
     int row, col;
     if (!TA) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
     else     { row = c / (BM / 4); col = (c % (BM / 4)) * 4; }
     *reinterpret_cast<f4 *>(as + row * A_LD + col) = ra[i];
   }
 #pragma unroll
-  for (int i = 0; i < BN * BK / 1024; ++i) {
-    const int c = tid + i * 256;
+  for (int i = 0; i < BN * BK / (4 * NT); ++i) {
+    const int c = tid + i * NT;
     int row, col;
     if (TB) { row = c / (BK / 4); col = (c % (BK / 4)) * 4; }
     else    { row = c / (BN / 4); col = (c % (BN / 4)) * 4; }
@@ -502,6 +508,347 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   }
   if (do_bias) bias_grad_store<BN>(p, ctx, smem, bsum, FULL);
   store_acc<BN, TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
+}
+
+// ---- 16x16x4 MFMA tiles --------------------------------------------------------
+// v_mfma_f32_16x16x4f32 (64 lanes): lane l supplies A[m = l%16][k = l/16] and
+// B[k = l/16][n = l%16]; accumulator v of lane l holds D[4*(l/16) + v][l%16].
+// Its 16-row granularity allows tiles of 96 = 3 x 32 rows and columns: a
+// [6144, 384] output is exactly 256 tiles of 96x96 (one per CU) where 64x64
+// tiles give 576 (2.25 per CU, and the CUs holding a third tile set the
+// time), and [6144, 1536] is 1024 (4 per CU) at 1.5x the operand reuse of a
+// 64x64 tile.
+
+// Epilogue of a block tile staged in LDS (ct: BM x BN, row stride BN + 4):
+// all 256 threads walk the tile row-major, float4 by float4, so each row of
+// the output is written by consecutive lanes (the 16x16 accumulator layout
+// would store 64-byte pieces of 4 rows). Raw into the split-K plane or a
+// tail split's partial tile, else through the epilogue with the arithmetic
+// and order of epilogue_store. With float4 access every group of 3 float4s
+// loads its epilogue operands (C, residual, GELU pre-activation) before its
+// stores, which might alias them.
+template <int BM, int BN, bool FULL, int NT = 256, int PARTS = 1>
+__device__ inline void tile_epilogue(const GemmParams &p, const BlockCtx &b, const float *ct) {
+  constexpr int C_LD = BN + 4, ROW4 = BN / 4, GROUPS = BM * ROW4, PER = (GROUPS + NT - 1) / NT;
+  constexpr int PART = BM * C_LD; // floats between the partial tiles (PARTS = 2)
+  static_assert(PARTS == 1 || PARTS == 2, "one tile or two partial tiles");
+  const int tid = threadIdx.x;
+  const bool raw = b.partial || p.splits > 1;
+  const int rs = b.partial ? BN : p.N;
+  float *rbase = b.partial ? b.C - (size_t(b.m0) * BN + b.n0) : b.C;
+  if (FULL && p.out_vec) {
+    constexpr int U = 3;
+#pragma unroll
+    for (int it0 = 0; it0 < PER; it0 += U) {
+      f4 v[U], cold[U], res[U], ax[U];
+      size_t oi[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = tid + (it0 + u) * NT;
+        cold[u] = res[u] = ax[u] = f4{0.f, 0.f, 0.f, 0.f};
+        oi[u] = 0;
+        if (it0 + u >= PER || e >= GROUPS) continue;
+        const int r = e / ROW4, c = (e - r * ROW4) * 4;
+        v[u] = *reinterpret_cast<const f4 *>(ct + r * C_LD + c);
+        if constexpr (PARTS == 2) v[u] += *reinterpret_cast<const f4 *>(ct + PART + r * C_LD + c);
+        const int m = b.m0 + r, n = b.n0 + c;
+        if (raw) {
+          oi[u] = size_t(m) * rs + n;
+        } else {
+          oi[u] = out_index(p, m, n);
+          if (p.beta != 0.0f) cold[u] = *reinterpret_cast<const f4 *>(b.C + oi[u]);
+          if (p.residual) res[u] = *reinterpret_cast<const f4 *>(p.residual + oi[u]);
+          if (p.epilogue == kEpiGeluBwd) ax[u] = *reinterpret_cast<const f4 *>(p.aux + oi[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = tid + (it0 + u) * NT;
+        if (it0 + u >= PER || e >= GROUPS) continue;
+        if (raw) {
+          *reinterpret_cast<f4 *>(rbase + oi[u]) = v[u];
+          continue;
+        }
+        const int r = e / ROW4, n = b.n0 + (e - r * ROW4) * 4;
+        f4 x = v[u];
+        if (b.bias) x += f4{b.bias[n], b.bias[n + 1], b.bias[n + 2], b.bias[n + 3]};
+        if (p.beta != 0.0f) x += p.beta * cold[u];
+        if (p.residual) x += res[u];
+        if (p.epilogue == kEpiGelu) {
+          *reinterpret_cast<f4 *>(p.aux + oi[u]) = x;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[q] = gelu_fwd(x[q]);
+        } else if (p.epilogue == kEpiGeluBwd) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[q] *= gelu_grad(ax[u][q]);
+        }
+        *reinterpret_cast<f4 *>(b.C + oi[u]) = x;
+      }
+    }
+  } else {
+    for (int e = tid; e < BM * BN; e += NT) {
+      const int r = e / BN, c = e - r * BN;
+      const int m = b.m0 + r, n = b.n0 + c;
+      if (!FULL && (m >= p.M || n >= p.N)) continue;
+      float v = ct[r * C_LD + c];
+      if constexpr (PARTS == 2) v += ct[PART + r * C_LD + c];
+      if (raw) rbase[size_t(m) * rs + n] = v;
+      else epilogue_store(p, b.bias, b.C, m, n, v);
+    }
+  }
+}
+
+// 4 waves in a 2x2 grid, each (BM/2) x (BN/2) as TM x TN subtiles of 16x16.
+// Within a K tile, lane group g = l/16 reads k = 4*(g + 4*s) + q for MFMA
+// step 4*s + q with one ds_read_b128 per s from a K-contiguous LDS row. With
+// a row stride of BK + 8 floats (an even, not a multiple of 4, number of
+// 16-byte groups) the 32 lanes of each read pass -- rows 0..15 of groups g
+// and g+1, one 16-byte group apart -- hit distinct banks of gfx950's LDS
+// (measured: no bank conflicts; with a stride of BK + 4, or consecutive k
+// blocks per lane group, 13% of the read cycles conflict). Same staging, K loop and epilogues as gemm_mfma_kernel; no
+// bias gradient (the planner keeps those on gemm_mfma_kernel).
+template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL>
+__global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  static_assert(WM % 16 == 0 && WN % 16 == 0 && BK % 16 == 0 && BK <= kBK, "tile geometry");
+  constexpr int A_LD = TA ? (BM + kPad) : (BK + kPad16);
+  constexpr int B_LD = TB ? (BK + kPad16) : (BN + kPad);
+  constexpr int A_TILE = TA ? BK * A_LD : BM * A_LD;
+  constexpr int B_TILE = TB ? BN * B_LD : BK * B_LD;
+  constexpr int A_CHUNKS = BM * BK / 1024, B_CHUNKS = BN * BK / 1024;
+  static_assert(A_CHUNKS * 1024 == BM * BK && B_CHUNKS * 1024 == BN * BK,
+                "every thread stages whole float4s of both operands");
+
+  __shared__ __attribute__((aligned(16))) float smem[2 * (A_TILE + B_TILE)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const int m0 = ctx.m0, n0 = ctx.n0;
+  const int k_begin = ctx.k_begin, k_end = ctx.k_end;
+  const float *A = ctx.A;
+  const float *B = ctx.B;
+
+  f4 ra[A_CHUNKS], rb[B_CHUNKS];
+  auto load_tile = [&](int k0) {
+    fetch_operands<BM, BN, BK, TA, TB, VEC, FULL>(p, A, B, m0, n0, k0, k_end, ra, rb);
+  };
+  auto store_tile = [&](int buf) {
+    float *as = smem + buf * (A_TILE + B_TILE);
+    stage_operands<BM, BN, BK, A_LD, B_LD, TA, TB>(as, as + A_TILE, ra, rb);
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int a_row0 = wm * WM + r16; // + i*16
+  const int b_col0 = wn * WN + r16; // + j*16
+
+  auto compute_tile = [&](int buf) {
+    const float *as = smem + buf * (A_TILE + B_TILE);
+    const float *bs = as + A_TILE;
+    constexpr int Q = BK / 16; // float4 groups per lane per K tile
+    f4 af[TM][Q], bf[TN][Q];
+#pragma unroll
+    for (int s4 = 0; s4 < Q; ++s4) {
+      const int kb = 4 * (g + 4 * s4); // first of 4 consecutive k
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = a_row0 + i * 16;
+        if (!TA) {
+          af[i][s4] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) af[i][s4][q] = as[(kb + q) * A_LD + m];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = b_col0 + j * 16;
+        if (TB) {
+          bf[j][s4] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bf[j][s4][q] = bs[(kb + q) * B_LD + n];
+        }
+      }
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < Q; ++s4)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s4][q], bf[j][s4][q],
+                                                             acc[i][j], 0, 0, 0);
+    if constexpr (!TA) __builtin_amdgcn_iglp_opt(1);
+  };
+
+  const int nk = (k_end > k_begin) ? (k_end - k_begin + BK - 1) / BK : 0;
+  if (nk > 0) {
+    load_tile(k_begin);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * BK);
+      compute_tile(cur);
+      if (kt + 1 < nk) store_tile(cur ^ 1);
+      __syncthreads();
+    }
+  }
+  // Accumulators -> LDS (free again: the K loop ended with a barrier), then
+  // the row-major epilogue. Lane l holds rows 4*(l/16) + v, column l%16 of
+  // each 16x16 subtile.
+  constexpr int C_LD = BN + 4;
+  static_assert(BM * C_LD <= 2 * (A_TILE + B_TILE), "output tile fits the operand buffers");
+  float *ct = smem;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ct[(wm * WM + i * 16 + 4 * g + v) * C_LD + wn * WN + j * 16 + r16] = acc[i][j][v];
+  __syncthreads();
+  tile_epilogue<BM, BN, FULL>(p, ctx, ct);
+}
+
+// 8 waves, 2 per SIMD, in two groups of 4. Each stage holds a K tile of 64
+// of both operands (staged by all 512 threads); group h multiplies k in
+// [32h, 32h + 32) of it into its own accumulators, as gemm_mfma16_kernel's
+// 2x2 waves do. A stage carries twice the MFMA work per barrier of the
+// 4-wave kernel, and a wave's LDS and barrier stalls overlap the other
+// group's MFMAs on its SIMD. The epilogue adds the two partial tiles (group
+// 0 + group 1). K tiles of 64: summed batch entries need 64 | seg_k, and
+// there is no split-K, tail split or bias gradient.
+template <int BM, int BN, bool TA, bool TB, bool VEC, bool FULL>
+__global__ __launch_bounds__(512) void gemm_mfma16x8_kernel(GemmParams p) {
+  constexpr int BK = 64, KH = 32, NT = 512;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "tile geometry");
+  constexpr int A_LD = TA ? (BM + kPad) : (BK + kPad16);
+  constexpr int B_LD = TB ? (BK + kPad16) : (BN + kPad);
+  constexpr int A_TILE = TA ? BK * A_LD : BM * A_LD;
+  constexpr int B_TILE = TB ? BN * B_LD : BK * B_LD;
+  constexpr int A_CHUNKS = BM * BK / (4 * NT), B_CHUNKS = BN * BK / (4 * NT);
+  static_assert(A_CHUNKS * 4 * NT == BM * BK && B_CHUNKS * 4 * NT == BN * BK,
+                "every thread stages whole float4s of both operands");
+  constexpr int C_LD = BN + 4;
+  static_assert(2 * BM * C_LD <= 2 * (A_TILE + B_TILE), "both partial tiles fit the operand buffers");
+
+  __shared__ __attribute__((aligned(16))) float smem[2 * (A_TILE + B_TILE)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave >> 2, wq = wave & 3;
+  const int wm = wq >> 1, wn = wq & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const int m0 = ctx.m0, n0 = ctx.n0;
+  const int k_begin = ctx.k_begin, k_end = ctx.k_end;
+  const float *A = ctx.A;
+  const float *B = ctx.B;
+
+  f4 ra[A_CHUNKS], rb[B_CHUNKS];
+  auto load_tile = [&](int k0) {
+    fetch_operands<BM, BN, BK, TA, TB, VEC, FULL, NT>(p, A, B, m0, n0, k0, k_end, ra, rb);
+  };
+  auto store_tile = [&](int buf) {
+    float *as = smem + buf * (A_TILE + B_TILE);
+    stage_operands<BM, BN, BK, A_LD, B_LD, TA, TB, NT>(as, as + A_TILE, ra, rb);
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int a_row0 = wm * WM + r16; // + i*16
+  const int b_col0 = wn * WN + r16; // + j*16
+  const int kg = grp * KH;          // the group's half of the stage
+
+  auto compute_tile = [&](int buf) {
+    const float *as = smem + buf * (A_TILE + B_TILE);
+    const float *bs = as + A_TILE;
+    constexpr int Q = KH / 16; // float4 groups per lane per half stage
+    f4 af[TM][Q], bf[TN][Q];
+#pragma unroll
+    for (int s4 = 0; s4 < Q; ++s4) {
+      const int kb = kg + 4 * (g + 4 * s4); // first of 4 consecutive k
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = a_row0 + i * 16;
+        if (!TA) {
+          af[i][s4] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) af[i][s4][q] = as[(kb + q) * A_LD + m];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = b_col0 + j * 16;
+        if (TB) {
+          bf[j][s4] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bf[j][s4][q] = bs[(kb + q) * B_LD + n];
+        }
+      }
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < Q; ++s4)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s4][q], bf[j][s4][q],
+                                                             acc[i][j], 0, 0, 0);
+    if constexpr (!TA) __builtin_amdgcn_iglp_opt(1);
+  };
+
+  const int nk = (k_end > k_begin) ? (k_end - k_begin + BK - 1) / BK : 0;
+  if (nk > 0) {
+    load_tile(k_begin);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * BK);
+      compute_tile(cur);
+      if (kt + 1 < nk) store_tile(cur ^ 1);
+      __syncthreads();
+    }
+  }
+  // Each group's partial tile -> LDS (group h at h * BM * C_LD), then the
+  // row-major epilogue over their sum.
+  float *ct = smem + grp * (BM * C_LD);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ct[(wm * WM + i * 16 + 4 * g + v) * C_LD + wn * WN + j * 16 + r16] = acc[i][j][v];
+  __syncthreads();
+  tile_epilogue<BM, BN, FULL, NT, 2>(p, ctx, smem);
 }
 
 
@@ -741,6 +1088,52 @@ void launch_cfg(const GemmParams &p, bool ta, bool tb, bool vec, bool full, dim3
 #undef TLH_GEMM_CASE
 }
 
+template <int BM, int BN>
+void launch16x8(const GemmParams &p, bool ta, bool tb, bool vec, bool full, dim3 grid,
+                hipStream_t s) {
+#define TLH_GEMM_CASE(TA_, TB_, V_, F_)                                             \
+  if (ta == TA_ && tb == TB_ && vec == V_ && full == F_) {                          \
+    gemm_mfma16x8_kernel<BM, BN, TA_, TB_, V_, F_><<<grid, 512, 0, s>>>(p);         \
+    return;                                                                         \
+  }
+  TLH_GEMM_CASE(false, false, true, true)
+  TLH_GEMM_CASE(false, true, true, true)
+  TLH_GEMM_CASE(true, false, true, true)
+  TLH_GEMM_CASE(true, true, true, true)
+  TLH_GEMM_CASE(false, false, true, false)
+  TLH_GEMM_CASE(false, true, true, false)
+  TLH_GEMM_CASE(true, false, true, false)
+  TLH_GEMM_CASE(true, true, true, false)
+  TLH_GEMM_CASE(false, false, false, false)
+  TLH_GEMM_CASE(false, true, false, false)
+  TLH_GEMM_CASE(true, false, false, false)
+  TLH_GEMM_CASE(true, true, false, false)
+#undef TLH_GEMM_CASE
+}
+
+template <int BM, int BN, int BK>
+void launch16(const GemmParams &p, bool ta, bool tb, bool vec, bool full, dim3 grid,
+              hipStream_t s) {
+#define TLH_GEMM_CASE(TA_, TB_, V_, F_)                                             \
+  if (ta == TA_ && tb == TB_ && vec == V_ && full == F_) {                          \
+    gemm_mfma16_kernel<BM, BN, BK, TA_, TB_, V_, F_><<<grid, 256, 0, s>>>(p);       \
+    return;                                                                         \
+  }
+  TLH_GEMM_CASE(false, false, true, true)
+  TLH_GEMM_CASE(false, true, true, true)
+  TLH_GEMM_CASE(true, false, true, true)
+  TLH_GEMM_CASE(true, true, true, true)
+  TLH_GEMM_CASE(false, false, true, false)
+  TLH_GEMM_CASE(false, true, true, false)
+  TLH_GEMM_CASE(true, false, true, false)
+  TLH_GEMM_CASE(true, true, true, false)
+  TLH_GEMM_CASE(false, false, false, false)
+  TLH_GEMM_CASE(false, true, false, false)
+  TLH_GEMM_CASE(true, false, false, false)
+  TLH_GEMM_CASE(true, true, false, false)
+#undef TLH_GEMM_CASE
+}
+
 inline size_t tiles_for(const GemmDesc &d, int bm, int bn) {
   return size_t((d.M + bm - 1) / bm) * size_t((d.N + bn - 1) / bn);
 }
@@ -786,7 +1179,21 @@ XcdRect xcd_rect(int tiles_m, int tiles_n) {
   return best;
 }
 int g_tail_split = 1;
+int g_tile96 = 1; // 96x96 tiles for tile-aligned products (see make_plan)
 constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
+
+bool vec_ok(const GemmDesc &d) {
+  auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int a_contig = d.trans_a ? d.M : d.K;
+  const int b_contig = d.trans_b ? d.K : d.N;
+  if (!al(d.A) || !al(d.B)) return false;
+  if (a_contig % 4 || b_contig % 4 || d.lda % 4 || d.ldb % 4) return false;
+  if (d.batch_ndim > 0) {
+    for (int i = 0; i < d.batch_ndim; ++i)
+      if (d.batch_stride_a[i] % 4 || d.batch_stride_b[i] % 4) return false;
+  }
+  return true;
+}
 
 // Tile plan, from measurements on MI355X of the GPT step's shapes
 // (M, N, K in {384, 1536, 2048, 6144}) and the d=1024 shapes:
@@ -815,7 +1222,30 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   const bool one_dim = d.sum_batches || d.batch_ndim <= 1;
   if (g_force_bm > 0) {
     const bool can_split = allow_split && one_dim;
+    if (g_force_bm == 96) { // 16x16 MFMA tiles, no bias gradient
+      if (d.bias_grad) return {64, 64, 1, 32};
+      // 8 waves over K tiles of 64: no split-K, summed entries of 64 | K
+      if (g_force_bk == 64 && (!d.sum_batches || d.K % 64 == 0)) return {96, 96, 1, 64};
+      return {96, 96, can_split ? std::max(1, g_force_splits) : 1, 32};
+    }
     return {g_force_bm, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, g_force_bk};
+  }
+  // 96x96 tiles on the 16x16x4 MFMA for tile-aligned outputs of 3/4 to 4
+  // tiles per CU: [6144, 384] is exactly one tile per CU where 64x64 tiles
+  // leave 64 CUs a third block (75% balance), [6144, 1536] four. At one
+  // tile per CU or fewer, 8 waves over K tiles of 64 (two wave groups per
+  // block: 25.0 -> 22.9 us at K = 384); above, 4 waves with two blocks
+  // co-resident per CU (N = 1536: 76.4 -> 69.2 us against 64x64).
+  // Measured on MI355X at M = 6144, N = 384 / 1536, K = 96 .. 3072, and the
+  // batched (3 x 256 tiles: 67.0 -> 64.4 us) and summed-batch Q/K/V forms.
+  if (g_tile96 && !d.bias_grad && !d.trans_a && vec_ok(d) && d.M % 96 == 0 && d.N % 96 == 0 &&
+      K % 32 == 0 && K >= 128) {
+    const size_t t96 = tiles_for(d, 96, 96) * outputs;
+    const size_t cus = size_t(cu_count());
+    const bool k64 = K % 64 == 0 && (!d.sum_batches || d.K % 64 == 0);
+    // (fewer tiles than about one per CU leave the product to split-K)
+    if (4 * t96 >= 3 * cus && t96 <= cus && k64) return {96, 96, 1, 64};
+    if (4 * t96 >= 3 * cus && t96 <= 4 * cus) return {96, 96, 1, 32};
   }
   // output area over the area of the tiles that cover it
   auto coverage = [&](int bm, int bn) {
@@ -843,18 +1273,6 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   return {64, 64, 1, K <= 256 ? 16 : 32};
 }
 
-bool vec_ok(const GemmDesc &d) {
-  auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const int a_contig = d.trans_a ? d.M : d.K;
-  const int b_contig = d.trans_b ? d.K : d.N;
-  if (!al(d.A) || !al(d.B)) return false;
-  if (a_contig % 4 || b_contig % 4 || d.lda % 4 || d.ldb % 4) return false;
-  if (d.batch_ndim > 0) {
-    for (int i = 0; i < d.batch_ndim; ++i)
-      if (d.batch_stride_a[i] % 4 || d.batch_stride_b[i] % 4) return false;
-  }
-  return true;
-}
 
 // One-row products that take the GEMV path: x [1, K], B [K, N] row-major
 // and float4-aligned, one batch dimension at most, no bias gradient.
@@ -916,7 +1334,8 @@ struct TailSplit {
 
 TailSplit tail_split(const GemmDesc &d, const Plan &plan, int K) {
   TailSplit t;
-  if (!g_tail_split || plan.splits > 1 || d.bias_grad || (d.batch > 1 && !d.sum_batches))
+  if (!g_tail_split || plan.splits > 1 || plan.bm == 96 || d.bias_grad ||
+      (d.batch > 1 && !d.sum_batches))
     return t;
   // the reduction launch costs a few microseconds: only long K ranges gain
   if (d.M % plan.bm || d.N % plan.bn || K % plan.bk || K < kMinTailSplitK) return t;
@@ -969,6 +1388,14 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   p.remap_t = d.remap_t; p.remap_h = d.remap_h; p.remap_d = d.remap_d;
   p.batch_ndim = d.batch_ndim;
   p.bias_bstride = d.bias_batch_stride;
+  {
+    auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    bool ov = al16(d.C) && (!d.residual || al16(d.residual)) && (!d.aux || al16(d.aux)) &&
+              (!d.workspace || al16(d.workspace)) && d.N % 4 == 0 &&
+              (d.remap_h > 0 ? d.remap_d % 4 == 0 : d.ldc % 4 == 0);
+    for (int i = 0; i < d.batch_ndim && i < 4; ++i) ov = ov && d.batch_stride_c[i] % 4 == 0;
+    p.out_vec = ov;
+  }
   p.batch = std::max(1, d.batch);
   int K = d.K;
   if (d.sum_batches) { // fold the batch into K: one product over batch*K
@@ -1035,7 +1462,11 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   // split chunk (a multiple of kBK) is.
   const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && K % plan.bk == 0 &&
                     (p.splits <= 1 || p.k_chunk % plan.bk == 0);
-  if (plan.bk == 32) {
+  if (plan.bm == 96 && plan.bk == 64) {
+    launch16x8<96, 96>(p, ta, tb, vec, full, grid, s);
+  } else if (plan.bm == 96) {
+    launch16<96, 96, 32>(p, ta, tb, vec, full, grid, s);
+  } else if (plan.bk == 32) {
     if (plan.bm == 128 && plan.bn == 128) launch_cfg<128, 128, 64, 64, 32>(p, ta, tb, vec, full, grid, s);
     else if (plan.bm == 128 && plan.bn == 64) launch_cfg<128, 64, 64, 32, 32>(p, ta, tb, vec, full, grid, s);
     else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64, 32>(p, ta, tb, vec, full, grid, s);
@@ -1111,7 +1542,8 @@ tlh::GemmDesc from_c(const tlh_gemm_desc &c) {
 TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   // bk < 0 toggles instead: the XCD-aware block order off (-1) or on (-2),
   // the tail split off (-3) or on (-4), the XCD rectangles off (-5) or on
-  // (-6).
+  // (-6), the one-row GEMV off (-7) or on (-8), the float4 split-K reduction
+  // off (-9) or on (-10), the planner's 96x96 tiles off (-11) or on (-12).
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
     return 0;
@@ -1132,8 +1564,14 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
     tlh::g_reduce4 = bk == -10;
     return 0;
   }
-  const bool ok = (bm == 0 && bn == 0) || ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
-  if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32)) return int(hipErrorInvalidValue);
+  if (bk == -11 || bk == -12) {
+    tlh::g_tile96 = bk == -12;
+    return 0;
+  }
+  const bool ok = (bm == 0 && bn == 0) || (bm == 96 && bn == 96 && (bk == 32 || bk == 64)) ||
+                  ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
+  if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32 && (bk != 64 || bm != 96)))
+    return int(hipErrorInvalidValue);
   tlh::g_force_bm = bm;
   tlh::g_force_bn = bn;
   tlh::g_force_splits = splits;

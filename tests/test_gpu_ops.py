@@ -219,8 +219,9 @@ def test_matmul(g, sa, sb):
 
 
 @pytest.mark.parametrize("sa,sb,splits", [
-    ((6144, 1536), (1536, 384), True),          # 576 tiles: tail split over K chunks
-    ((32, 192, 1536), (1536, 384), True),       # weight broadcast, folded into one product
+    ((6144, 1536), (1536, 448), True),          # 672 tiles of 64x64: tail split over K chunks
+    ((32, 192, 1536), (1536, 448), True),       # weight broadcast, folded into one product
+    ((6144, 1536), (1536, 384), False),         # 256 tiles of 96x96: no scratch
     ((384, 6144), (6144, 384), True),           # 36 tiles: split-K
     ((32, 384, 192), (32, 192, 384), False),    # per-sample weight grad: no scratch
     ((1, 1024), (1024, 512), True),             # one row: GEMV chunks
@@ -338,6 +339,7 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -6), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -8), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -10), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -12), "set_plan")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
@@ -419,7 +421,9 @@ def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
 def test_gemm_tail_split(g, forced_plan, ta, tb, K):
     # 6144 x 384 is 576 tiles of 64x64: 512 whole-K blocks (2 per CU) and
     # 64 tiles cut into K chunks summed afterwards. Same result with the
-    # tail split off, bit-identical run to run, every epilogue input.
+    # tail split off, bit-identical run to run, every epilogue input. (The
+    # planner's 96x96 tiles, one per CU, are switched off.)
+    forced_plan(0, 0, 0, -11)
     M, N = 6144, 384
     a = O.normal((K, M) if ta else (M, K), 160, 0, 0.5)
     b = O.normal((N, K) if tb else (K, N), 161, 0, 0.5)
@@ -434,9 +438,10 @@ def test_gemm_tail_split(g, forced_plan, ta, tb, K):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
-def test_gemm_tail_split_gelu_epilogues(g):
+def test_gemm_tail_split_gelu_epilogues(g, forced_plan):
     # the tail tiles' reduction applies the GELU forward (writing the
     # pre-activation) and the GELU' epilogue like the whole-K blocks do
+    forced_plan(0, 0, 0, -11)  # 64x64 tiles (576, so a tail split)
     M, N, K = 6144, 384, 1536
     a, b = O.normal((M, K), 165, 0, 0.05), O.normal((K, N), 166, 0, 0.05)
     bias = O.normal((N,), 167)
@@ -585,6 +590,69 @@ def test_gemm_summed_batches(g, M, N, K):
     c0, res, bias = O.normal((M, N), 144), O.normal((M, N), 145), O.normal((N,), 146)
     keep = []
     da, dw, dc = g.dev(a), g.dev(w), g.dev(c0)
+    d = _batched_desc(da, dw, dc, False, True, M, N, K, 3, M * K, N * K, 0)
+    d.sum_batches = 1
+    d.beta = 1.0
+    dres, dbias = g.dev(res), g.dev(bias)
+    d.residual, d.bias = dres.data_ptr(), dbias.data_ptr()
+    _with_workspace(g, keep, d)
+    g.call("tlh_gemm", ctypes.byref(d))
+    expect = sum(O.matmul(a[j], w[j].T) for j in range(3)) + c0 + res + bias
+    assert_rel(g.host(dc).reshape(M, N), expect, 1e-3, "summed")
+
+
+@pytest.mark.parametrize("bk", [32, 64])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_tile96(g, forced_plan, ta, tb, bk):
+    # 96x96 tiles on the 16x16x4 MFMA: every operand layout on the step's
+    # [6144,384] product (exactly 256 tiles), every epilogue, the head-layout
+    # store (96-column tiles straddle the 64-wide heads), the batched and
+    # summed-batch (K-segmented) forms and the bounds-checked ragged path.
+    # bk 32: 4 waves; bk 64: 8 waves in two K groups over K tiles of 64.
+    forced_plan(96, 96, 1, bk)
+    M, N, K = 6144, 384, 384
+    a = O.normal((K, M) if ta else (M, K), 180, 0, 0.5)
+    b = O.normal((N, K) if tb else (K, N), 181, 0, 0.5)
+    prod = O.matmul(a.T if ta else a, b.T if tb else b)
+    out, _ = gemm(g, a, b, ta, tb)
+    assert_rel(out.reshape(M, N), prod, 1e-3, "plain")
+    bias, res, c0 = O.normal((N,), 182), O.normal((M, N), 183), O.normal((M, N), 184)
+    out, _ = gemm(g, a, b, ta, tb, bias=bias, residual=res, beta=1.0, c_init=c0)
+    assert_rel(out.reshape(M, N), prod + bias + c0 + res, 1e-3, "bias+residual+beta")
+    out, pre = gemm(g, a, b, ta, tb, bias=bias, epi=EPI_GELU)
+    u = O.binary("add", prod, bias.reshape(1, N))
+    assert_rel(pre.reshape(M, N), u, 1e-3, "gelu pre-activation")
+    assert_rel(out.reshape(M, N), O.unary("gelu", u), 1e-3, "gelu")
+    out, _ = gemm(g, a, b, ta, tb, epi=EPI_GELU_BWD, aux=u)
+    assert_rel(out.reshape(M, N), prod * O.unary("gelu_derivative", u), 1e-3, "gelu'")
+    if not ta:
+        T, H, D = 192, 6, 64
+        out, _ = gemm(g, a, b, ta, tb, bias=bias, remap=(T, H, D))
+        y = O.binary("add", prod, bias.reshape(1, -1)).reshape(M // T, T, H, D)
+        assert_rel(out.reshape(M // T, H, T, D), y.transpose(0, 2, 1, 3), 1e-3, "head remap")
+    # ragged edges: bounds-checked loads and stores
+    a2 = O.normal((100, 200) if ta else (200, 100), 185, 0, 0.5)
+    b2 = O.normal((300, 100) if tb else (100, 300), 186, 0, 0.5)
+    out, _ = gemm(g, a2, b2, ta, tb)
+    assert_rel(out.reshape(200, 300), O.matmul(a2.T if ta else a2, b2.T if tb else b2), 1e-3,
+               "ragged")
+
+
+@pytest.mark.parametrize("bk", [32, 64])
+def test_gemm_tile96_batched_and_summed(g, forced_plan, bk):
+    forced_plan(96, 96, 1, bk)
+    M, N, K = 960, 192, 384
+    a = O.normal((3, M, K), 187, 0, 0.5)
+    w = O.normal((3, N, K), 188, 0, 0.5)
+    keep = []
+    da, dw, dc = g.dev(a), g.dev(w), g.zeros((3 * M * N,))
+    d = _batched_desc(da, dw, dc, False, True, M, N, K, 3, M * K, N * K, M * N)
+    g.call("tlh_gemm", ctypes.byref(d))
+    got = g.host(dc).reshape(3, M, N)
+    for j in range(3):
+        assert_rel(got[j], O.matmul(a[j], w[j].T), 1e-3, f"batched[{j}]")
+    c0, res, bias = O.normal((M, N), 189), O.normal((M, N), 190), O.normal((N,), 191)
+    dc = g.dev(c0)
     d = _batched_desc(da, dw, dc, False, True, M, N, K, 3, M * K, N * K, 0)
     d.sum_batches = 1
     d.beta = 1.0

@@ -52,7 +52,7 @@ def both(g, a, b, seed_out):
 # (first, second): the second call is the smaller one
 CASES = [
     ((384, 6144, 2048), (384, 6144, 384)),   # split-K: 4 then 8 splits of [384, N]
-    ((6144, 1536, 384), (384, 6144, 384)),   # tail split, then split-K
+    ((6144, 1536, 448), (384, 6144, 384)),   # tail split (672 tiles of 64x64), then split-K
     ((1, 4096, 1024), (1, 1024, 512)),       # one-row GEMV chunks
     ((384, 6144, 384), (256, 256, 256)),     # split-K, then a plan without scratch
 ]
