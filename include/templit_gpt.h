@@ -121,6 +121,21 @@ int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t pro
                         uint32_t n_new, uint32_t eos_token, int prefix_only,
                         uint32_t *host_out);
 
+/* Sampled autoregressive generation, inference::autoregression
+ * (include/inference.h:45-99) with inference::sample_top_k (14-43) on the
+ * device (tlh_sample_top_k): the window and the three prefix_only modes are
+ * tlg_generate_greedy's; each step samples the next token from the top_k
+ * logits at temperature `temperature`, drawing again while it is eos_token
+ * and fewer than min(minimum_length, seq) tokens were generated, and
+ * generation ends after an emitted eos_token or n_new tokens. Uniforms come
+ * from the SplitMix64 stream seeded with `seed`, each draw taking the next
+ * output (the reference's std::mt19937 is a host-side choice). The tokens
+ * go to host_out, their number to *host_count. Synchronous. */
+int tlg_generate_sample(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
+                        uint32_t n_new, uint32_t eos_token, uint32_t top_k, float temperature,
+                        uint32_t minimum_length, uint64_t seed, int prefix_only,
+                        uint32_t *host_out, uint32_t *host_count);
+
 /* Squared gradient norm of the last step (host read, synchronous). */
 int tlg_last_squared_norm(void *program, float *host_value);
 

@@ -352,6 +352,28 @@ int tlh_max_to_shape(const float *a, float *out, uint32_t ndim,
 /* argmax (math.metal:715-777, runtime.cpp:850-918): index of the first
  * maximum (lowest index on ties; NaNs never win). n >= 1. */
 int tlh_argmax(const float *a, size_t n, uint32_t *out_index, void *stream);
+/* Top-k sampling with temperature, one row at a time on the device:
+ * inference::sample_top_k (include/inference.h:14-43) -- candidates are the
+ * top_k (clamped to [1, vocab]) largest logits, descending (equal logits:
+ * lower token first, where the reference's partial_sort leaves the order
+ * unspecified; NaN ranks as -INF), weights exp((l_i - l_0) / temperature)
+ * in fp32 and std::discrete_distribution's draw (cumulative sums of w_i / S
+ * in double, the last set to 1, the first >= u) -- plus the EOS re-draw of
+ * inference::autoregression (inference.h:80-84): with resample_eos a draw
+ * that yields eos_token is repeated with the next uniform, at most
+ * max_draws draws (then the last result stands; the reference would loop
+ * on). Uniform d of row r is uniforms[r * max_draws + d] when `uniforms`
+ * (device, rows * max_draws doubles in [0, 1)) is given -- e.g. the
+ * generate_canonical<double, 53> draws of the reference's std::mt19937 --
+ * else output number counter + r * max_draws + d + 1 of the SplitMix64
+ * stream seeded with `seed`, as (x >> 11) * 2^-53. tokens[r] = the token;
+ * draws[r] (optional) = the draws used. 1 <= vocab <= 4096; temperature
+ * finite and > 0; row_stride >= vocab when rows > 1 (0 with one row is
+ * ignored). */
+int tlh_sample_top_k(const float *logits, uint32_t rows, uint32_t vocab, uint32_t row_stride,
+                     uint32_t top_k, float temperature, uint64_t seed, uint64_t counter,
+                     const double *uniforms, uint32_t eos_token, int resample_eos,
+                     uint32_t max_draws, uint32_t *tokens, uint32_t *draws, void *stream);
 /* Row argmax: out[r] = argmax over a[r, 0:cols] (greedy decoding). */
 int tlh_argmax_rows(const float *a, size_t rows, uint32_t cols,
                     uint32_t *out_index, void *stream);

@@ -266,6 +266,67 @@ uint32_t orc_argmax(const float *a, size_t n) {
   return index;
 }
 
+// Top-k sampling, inference::sample_top_k (include/inference.h:14-43): the
+// candidates (logit, token) are ordered by logit, descending (partial_sort
+// with a.first > b.first; its order of equal logits is unspecified, here the
+// lower token comes first), weights are std::exp((logit - maximum) /
+// temperature) in fp32 (the exponential taken in double and rounded to fp32,
+// the correctly rounded expf), and std::discrete_distribution picks one:
+// libstdc++ normalises each weight by the double sum, takes partial sums,
+// sets the last to 1.0 and returns the lower_bound of one
+// generate_canonical<double, 53> draw. The EOS re-draw loop is
+// inference::autoregression's (inference.h:80-84), bounded by max_draws.
+void orc_sample_top_k(const float *logits, uint32_t rows, uint32_t vocab, uint32_t row_stride,
+                      uint32_t top_k, float temperature, uint64_t seed, uint64_t counter,
+                      const double *uniforms, uint32_t eos_token, int resample_eos,
+                      uint32_t max_draws, uint32_t *tokens, uint32_t *draws) {
+  const uint32_t k = std::min(std::max(top_k, 1u), vocab);
+  std::vector<std::pair<float, uint32_t>> cand(vocab);
+  std::vector<float> w(k);
+  for (uint32_t r = 0; r < rows; ++r) {
+    const float *row = logits + size_t(r) * row_stride;
+    for (uint32_t t = 0; t < vocab; ++t) {
+      const float x = row[t];
+      cand[t] = {std::isnan(x) ? -std::numeric_limits<float>::infinity() : x, t};
+    }
+    std::sort(cand.begin(), cand.end(), [](const auto &a, const auto &b) {
+      return a.first > b.first || (a.first == b.first && a.second < b.second);
+    });
+    const float maximum = cand[0].first;
+    double total = 0.0;
+    for (uint32_t i = 0; i < k; ++i) {
+      w[i] = float(std::exp(double((cand[i].first - maximum) / temperature)));
+      total += double(w[i]);
+    }
+    uint32_t token = 0, d = 0;
+    for (; d < max_draws; ++d) {
+      double u;
+      if (uniforms) {
+        u = uniforms[size_t(r) * max_draws + d];
+      } else {
+        SplitMix64 g{seed + (counter + uint64_t(r) * max_draws + d) * 0x9E3779B97F4A7C15ull};
+        u = double(g.next() >> 11) * (1.0 / 9007199254740992.0);
+      }
+      uint32_t pick = k - 1;
+      double c = 0.0;
+      for (uint32_t i = 0; i + 1 < k; ++i) {
+        c += double(w[i]) / total;
+        if (c >= u) {
+          pick = i;
+          break;
+        }
+      }
+      token = cand[pick].second;
+      if (!(resample_eos && token == eos_token)) {
+        ++d;
+        break;
+      }
+    }
+    tokens[r] = token;
+    if (draws) draws[r] = std::min(d, max_draws);
+  }
+}
+
 // softmax per row: max, shift, exp, serial sum, divide (cpu.cpp:501-519).
 void orc_softmax(const float *x, float *out, size_t rows, uint32_t cols) {
   std::vector<float> e(cols);

@@ -97,6 +97,25 @@ void orc_attention_backward(const float *q, const float *k, const float *v,
                             const float *probs, const float *dout, float *dq, float *dk,
                             float *dv, uint32_t B, uint32_t H, uint32_t T, uint32_t D);
 
+/* ---- top-k sampling (include/inference.h:14-43, 80-84) ----
+ * Per row: the top_k (clamped to [1, vocab]) largest logits in descending
+ * order (equal logits: lower token first; NaN ranks as -INF), weights
+ * w_i = exp((l_i - l_0) / temperature) with the difference and quotient in
+ * fp32 and the exponential rounded to fp32 from double, then the
+ * discrete_distribution draw: cumulative sums of w_i / S in double
+ * (S = the double sum of the w_i in order), the last set to 1, and the first
+ * candidate whose cumulative sum is >= u. Draw d of row r uses
+ * u = uniforms[r * max_draws + d] when uniforms is given, else the
+ * (counter + r * max_draws + d + 1)-th output x of the SplitMix64 stream
+ * seeded with `seed`, as (x >> 11) * 2^-53. With resample_eos, a draw that
+ * yields eos_token is repeated with the next u, at most max_draws draws in
+ * all (the last result stands). tokens[r] = the token, draws[r] = the draws
+ * used. */
+void orc_sample_top_k(const float *logits, uint32_t rows, uint32_t vocab, uint32_t row_stride,
+                      uint32_t top_k, float temperature, uint64_t seed, uint64_t counter,
+                      const double *uniforms, uint32_t eos_token, int resample_eos,
+                      uint32_t max_draws, uint32_t *tokens, uint32_t *draws);
+
 /* ---- GPT training step (include/nn/GPT.h, src/train.cpp loop body) ---- */
 typedef struct orc_gpt_config {
   uint32_t vocab, seq, dim, heads, layers, batch, ffn;

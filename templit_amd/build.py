@@ -55,6 +55,7 @@ KERNEL_SOURCES = [
     "embedding.hip",
     "attention.hip",
     "optim.hip",
+    "sample.hip",
 ]
 
 RUNTIME_SOURCES = [

@@ -48,6 +48,9 @@ constexpr uint32_t kHeadDim = 64;
 constexpr float kRmsEps = 1e-6f; // src/my_metal/runtime.cpp:1044
 constexpr size_t kAlign = 64;    // floats: every tensor starts 256-byte aligned
 constexpr int kInvalidValue = 1; // hipErrorInvalidValue
+// EOS re-draws per sampled token before the last draw stands (the reference
+// draws until a non-EOS token comes, inference.h:80-84)
+constexpr uint32_t kMaxSampleDraws = 1024;
 
 struct Program {
   tlg_config cfg{};
@@ -611,7 +614,7 @@ int create(Program &p) {
   TRY(tlh_fill_u32(p.tokens, 0, R, p.stream));
   TRY(tlh_fill_u32(p.targets, 0, R, p.stream));
   TRY(allocf(p, &p.losses, R));
-  TRY(alloc(p, reinterpret_cast<void **>(&p.argmax_out), sizeof(uint32_t)));
+  TRY(alloc(p, reinterpret_cast<void **>(&p.argmax_out), 2 * sizeof(uint32_t)));
   TRY(allocf(p, &p.logits, R * V));
   TRY(allocf(p, &p.dlogits, R * V));
   p.x.resize(L + 1);
@@ -948,62 +951,102 @@ int tlg_forward(void *program) {
   return forward(p, p.cfg.seq);
 }
 
-int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
-                        uint32_t n_new, uint32_t eos_token, int prefix_only,
-                        uint32_t *host_out) {
-  Program &p = *static_cast<Program *>(program);
+extern "C++" {
+namespace {
+// inference::autoregression's loop (include/inference.h:45-99): the window
+// holds the prompt, EOS-padded; each step computes the logits at the last
+// valid position, `choose` launches the kernel that writes the next token
+// (and the draws it used) to p.argmax_out[0..1], and the token is appended
+// (the window slides once full). With stop_at_eos generation ends after an
+// EOS is emitted (inference.h:86-90). prefix_only: 0 recomputes the padded
+// window as the reference does, 1 only the valid prefix (the same logits:
+// attention is causal), 2 keeps the window's K/V planes and runs each new
+// position alone through decode_step while the window has room. `picked`
+// sees each step's token and draw count. Returns the tokens generated in
+// *count.
+template <typename Choose, typename Picked>
+int generate(Program &p, const uint32_t *host_prompt, uint32_t prompt_len, uint32_t n_new,
+             uint32_t eos_token, int prefix_only, bool stop_at_eos, Choose &&choose,
+             Picked &&picked, uint32_t *host_out, uint32_t *count) {
   const tlg_config &c = p.cfg;
-  if (c.batch != 1 || prompt_len == 0 || prompt_len > c.seq) return kInvalidValue;
+  *count = 0;
+  if (c.batch != 1 || prompt_len == 0 || prompt_len > c.seq || prefix_only < 0 ||
+      prefix_only > 2)
+    return kInvalidValue;
   for (uint32_t i = 0; i < prompt_len; ++i)
     if (host_prompt[i] >= c.vocab) return kInvalidValue;
-  // inference::autoregression (include/inference.h:45-99): the window holds
-  // the prompt, EOS-padded; each step recomputes the forward, predicts at
-  // the last valid position and appends (sliding once the window is full).
-  // Greedy = the lowest-index maximum of the logits; EOS does not stop it.
   std::vector<uint32_t> context(c.seq, eos_token);
   std::copy(host_prompt, host_prompt + prompt_len, context.begin());
   uint32_t valid = prompt_len;
-  // prefix_only == 2 (KV cache): after the first window forward, each new
-  // position runs through decode_step alone while the window has room.
   bool cached = false;
-  auto next_token = [&](uint32_t &token) -> int {
-    TRY(tlh_memcpy_d2h(&token, p.argmax_out, sizeof(token), p.stream));
-    return tlh_stream_synchronize(p.stream);
-  };
   for (uint32_t g = 0; g < n_new; ++g) {
+    const float *row;
     if (cached) {
       const uint32_t t = valid - 1; // the newest token's position
       TRY(tlh_memcpy_h2d(p.tokens + t, &context[t], sizeof(uint32_t), p.stream));
       TRY(decode_step(p, t));
-      TRY(tlh_argmax(p.logits, c.vocab, p.argmax_out, p.stream));
-      uint32_t token = 0;
-      TRY(next_token(token));
-      host_out[g] = token;
-      if (valid < c.seq) {
-        context[valid++] = token;
-      } else {
-        std::move(context.begin() + 1, context.end(), context.begin());
-        context.back() = token;
-        cached = false; // the window slid: every position moved
-      }
-      continue;
+      row = p.logits;
+    } else {
+      const uint32_t seq = prefix_only == 1 ? valid : c.seq;
+      TRY(tlh_memcpy_h2d(p.tokens, context.data(), size_t(seq) * sizeof(uint32_t), p.stream));
+      TRY(forward(p, seq));
+      row = p.logits + size_t(valid - 1) * c.vocab;
     }
-    const uint32_t seq = prefix_only == 1 ? valid : c.seq;
-    TRY(tlh_memcpy_h2d(p.tokens, context.data(), size_t(seq) * sizeof(uint32_t), p.stream));
-    TRY(forward(p, seq));
-    TRY(tlh_argmax(p.logits + size_t(valid - 1) * c.vocab, c.vocab, p.argmax_out, p.stream));
-    uint32_t token = 0;
-    TRY(next_token(token));
+    TRY(choose(row, g));
+    uint32_t out[2] = {0, 0};
+    TRY(tlh_memcpy_d2h(out, p.argmax_out, sizeof(out), p.stream));
+    TRY(tlh_stream_synchronize(p.stream));
+    const uint32_t token = out[0];
     host_out[g] = token;
+    *count = g + 1;
+    picked(token, out[1]);
+    if (stop_at_eos && token == eos_token) break;
     if (valid < c.seq) {
       context[valid++] = token;
-      cached = prefix_only == 2; // the window's K/V planes now serve decode_step
+      // the window's K/V planes now serve decode_step (or keep serving it)
+      cached = prefix_only == 2;
     } else {
       std::move(context.begin() + 1, context.end(), context.begin());
       context.back() = token;
+      cached = false; // the window slid: every position moved
     }
   }
   return 0;
+}
+} // namespace
+} // extern "C++"
+
+int tlg_generate_greedy(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
+                        uint32_t n_new, uint32_t eos_token, int prefix_only,
+                        uint32_t *host_out) {
+  Program &p = *static_cast<Program *>(program);
+  uint32_t count = 0;
+  // greedy = the lowest-index maximum of the logits (sample_top_k with
+  // top_k 1); EOS does not stop it
+  return generate(
+      p, host_prompt, prompt_len, n_new, eos_token, prefix_only, false,
+      [&](const float *row, uint32_t) { return tlh_argmax(row, p.cfg.vocab, p.argmax_out, p.stream); },
+      [](uint32_t, uint32_t) {}, host_out, &count);
+}
+
+int tlg_generate_sample(void *program, const uint32_t *host_prompt, uint32_t prompt_len,
+                        uint32_t n_new, uint32_t eos_token, uint32_t top_k, float temperature,
+                        uint32_t minimum_length, uint64_t seed, int prefix_only,
+                        uint32_t *host_out, uint32_t *host_count) {
+  Program &p = *static_cast<Program *>(program);
+  if (!host_count || !(temperature > 0.0f)) return kInvalidValue;
+  // inference.h:68, 80-84: EOS is drawn again while fewer than
+  // min(minimum_length, window) tokens were generated
+  const uint32_t min_len = std::min(minimum_length, p.cfg.seq);
+  uint64_t counter = 0; // SplitMix64 outputs used so far
+  return generate(
+      p, host_prompt, prompt_len, n_new, eos_token, prefix_only, true,
+      [&](const float *row, uint32_t g) {
+        return tlh_sample_top_k(row, 1, p.cfg.vocab, p.cfg.vocab, top_k, temperature, seed,
+                                counter, nullptr, eos_token, g < min_len ? 1 : 0,
+                                kMaxSampleDraws, p.argmax_out, p.argmax_out + 1, p.stream);
+      },
+      [&](uint32_t, uint32_t used) { counter += used; }, host_out, host_count);
 }
 
 int tlg_last_squared_norm(void *program, float *host_value) {

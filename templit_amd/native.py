@@ -124,6 +124,8 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_max_to_shape": [P, P, c_uint32, U32P, U32P, P],
     "tlh_argmax": [P, c_size_t, P, P],
     "tlh_argmax_rows": [P, c_size_t, c_uint32, P, P],
+    "tlh_sample_top_k": [P, c_uint32, c_uint32, c_uint32, c_uint32, c_float, c_uint64, c_uint64,
+                         P, c_uint32, c_int, c_uint32, P, P, P],
     "tlh_accumulate_gradient_squared_norm": [P, c_size_t, P, P],
     "tlh_gradient_squared_norm_multi": [P, P, c_uint32, P, P, P],
     "tlh_column_sum": [P, c_size_t, c_uint32, P, c_float, P],
@@ -234,6 +236,8 @@ GPT_SIGNATURES: dict[str, list] = {
     "tlg_train_step": [P, c_float, c_float, c_int],
     "tlg_forward": [P],
     "tlg_generate_greedy": [P, P, c_uint32, c_uint32, c_uint32, c_int, P],
+    "tlg_generate_sample": [P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_float, c_uint32,
+                            c_uint64, c_int, P, POINTER(c_uint32)],
     "tlg_last_squared_norm": [P, POINTER(c_float)],
     "tlg_profile_step": [P, c_float, c_float, POINTER(c_float), POINTER(ctypes.c_double),
                          POINTER(ctypes.c_double), POINTER(c_uint32), POINTER(c_float),
@@ -462,6 +466,19 @@ class GptProgram:
         check(self.lib.tlg_generate_greedy(self.handle, pr.ctypes.data, pr.size, n_new, eos_token,
                                            int(prefix_only), out.ctypes.data), "generate")
         return out
+
+    def generate_sample(self, prompt, n_new, eos_token, top_k, temperature, minimum_length,
+                        seed, prefix_only=0):
+        """Top-k sampled generation (tlg_generate_sample): the tokens up to and
+        including an emitted EOS, at most n_new."""
+        pr = self._np.ascontiguousarray(prompt, dtype=self._np.uint32)
+        out = self._np.empty(n_new, self._np.uint32)
+        count = c_uint32()
+        check(self.lib.tlg_generate_sample(self.handle, pr.ctypes.data, pr.size, n_new, eos_token,
+                                           top_k, temperature, minimum_length, seed,
+                                           int(prefix_only), out.ctypes.data,
+                                           ctypes.byref(count)), "generate_sample")
+        return out[:count.value]
 
     def capture(self, root_grad, max_norm):
         check(self.lib.tlg_capture_train_step(self.handle, root_grad, max_norm), "capture")

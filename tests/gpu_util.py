@@ -26,6 +26,9 @@ class Gpu:
             return torch.from_numpy(a.view(np.int32)).to("cuda")
         return torch.from_numpy(a.astype(np.float32, copy=False)).to("cuda")
 
+    def dev_f64(self, a) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float64)).to("cuda")
+
     def empty(self, shape, dtype=torch.float32) -> torch.Tensor:
         return torch.empty(tuple(shape), dtype=dtype, device="cuda")
 

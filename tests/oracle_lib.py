@@ -76,6 +76,8 @@ def _load_oracle() -> ctypes.CDLL:
         "orc_gpt_train_step": [POINTER(GptConfig), V, V, V, c_uint32, V, V, c_float, c_float,
                                c_float, c_float, c_float, c_float, c_float, V, V, V],
         "orc_gpt_forward": [POINTER(GptConfig), V, V, V],
+        "orc_sample_top_k": [V, c_uint32, c_uint32, c_uint32, c_uint32, c_float, c_uint64,
+                             c_uint64, V, c_uint32, c_int, c_uint32, V, V],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -250,6 +252,24 @@ def total_sum(a: np.ndarray) -> float:
 def argmax(a: np.ndarray) -> int:
     a = _f32(a)
     return int(lib().orc_argmax(p(a), a.size))
+
+
+def sample_top_k(logits: np.ndarray, top_k: int, temperature: float, seed: int = 0,
+                 counter: int = 0, uniforms=None, eos: int = 0, resample_eos: bool = False,
+                 max_draws: int = 1, row_stride: int | None = None):
+    """orc_sample_top_k over the rows of `logits` ([rows, V], or [V] for one
+    row): (tokens u32 [rows], draws u32 [rows])."""
+    x = _f32(logits)
+    V = x.shape[-1]
+    rows = x.size // V if row_stride is None else len(uniforms) // max_draws
+    stride = V if row_stride is None else row_stride
+    tokens = np.zeros(rows, np.uint32)
+    draws = np.zeros(rows, np.uint32)
+    u = None if uniforms is None else np.ascontiguousarray(uniforms, dtype=np.float64)
+    lib().orc_sample_top_k(p(x), rows, V, stride, top_k, temperature, seed, counter,
+                           None if u is None else p(u), eos, int(resample_eos), max_draws,
+                           p(tokens), p(draws))
+    return tokens, draws
 
 
 def softmax(x: np.ndarray) -> np.ndarray:

@@ -457,6 +457,71 @@ def test_greedy_generation_matches_oracle(prefix_only):
     assert _greedy_reference_check(cfg, params, prompt, out, eos) >= 38
 
 
+def _sample_reference_check(cfg, params, prompt, generated, eos, top_k, temperature,
+                            min_len, seed):
+    """Replays sampled generation with the oracle: each step's logits from
+    the oracle's forward, the oracle's sampler on the same SplitMix64
+    stream (each draw takes the next output; EOS drawn again while fewer than
+    min_len tokens were generated), generation ending after an EOS. The GPU's
+    logits differ from the oracle's by rounding only, so the tokens agree
+    unless a draw lands within that rounding of a cumulative boundary."""
+    context = np.full(cfg.seq, eos, np.uint32)
+    context[:len(prompt)] = prompt
+    valid, counter, expect = len(prompt), 0, []
+    for g in range(len(generated)):
+        logits = O.gpt_forward(cfg, params, context)[valid - 1]
+        tok, used = O.sample_top_k(logits, top_k, temperature, seed, counter, eos=eos,
+                                   resample_eos=g < min(min_len, cfg.seq), max_draws=1024)
+        counter += int(used[0])
+        expect.append(int(tok[0]))
+        if tok[0] == eos:
+            break
+        if valid < cfg.seq:
+            context[valid] = tok[0]
+            valid += 1
+        else:
+            context = np.roll(context, -1)
+            context[-1] = tok[0]
+    return expect
+
+
+@pytest.mark.parametrize("prefix_only", [0, 1, 2])  # 2: KV cache
+def test_sampled_generation_matches_oracle(prefix_only):
+    V, T, D, H, L = 96, 32, 128, 2, 2
+    cfg = O.gpt_config(V, T, D, H, L, 1)
+    total = int(sum(O.gpt_param_sizes(cfg)))
+    params = O.normal((total,), 620, 0, 0.2)
+    prompt = O.uniform_u32((5,), 621, V)
+    prog = GptProgram(V, T, D, H, L, 1)
+    try:
+        prog.set_params(params)
+        runs = {}
+        # (eos, top_k, temperature, minimum length, seed): the most likely
+        # first token as EOS with a long minimum (the re-draw and the window
+        # slide), a rarely drawn EOS, and a short run ended by EOS
+        for case in ((None, 8, 0.9, 40, 31), (95, 40, 1.2, 0, 32), (None, 3, 3.0, 2, 33)):
+            eos, k, t, m, seed = case
+            if eos is None:
+                eos = int(O.argmax(O.gpt_forward(cfg, params, np.concatenate(
+                    [prompt, np.zeros(T - 5, np.uint32)]))[4]))
+            out = prog.generate_sample(prompt, 40, eos, k, t, m, seed, prefix_only=prefix_only)
+            runs[case] = out
+            assert 1 <= len(out) <= 40 and np.all(out < V)
+            if len(out) < 40:
+                assert out[-1] == eos and not np.any(out[:-1] == eos)
+            # no EOS before min(minimum length, window) tokens (inference.h:68)
+            assert not np.any(out[:min(m, T)] == eos)
+            assert list(out) == _sample_reference_check(cfg, params, prompt, out, eos, k, t, m,
+                                                        seed)
+        # top_k 1 is greedy: the same tokens as tlg_generate_greedy up to EOS
+        greedy = prog.generate_greedy(prompt, 40, 95, prefix_only=prefix_only)
+        top1 = prog.generate_sample(prompt, 40, 95, 1, 0.7, 0, 5, prefix_only=prefix_only)
+        n = len(top1)
+        np.testing.assert_array_equal(top1, greedy[:n])
+    finally:
+        prog.close()
+
+
 def test_greedy_prefix_equals_full_window():
     V, T, D, H, L = 64, 48, 128, 2, 2
     cfg = O.gpt_config(V, T, D, H, L, 1)

@@ -768,6 +768,81 @@ def test_argmax_kats(g):
         assert int(g.host(out)[0]) == O.argmax(x)
 
 
+# ---------------------------------------------------------------------------
+# top-k sampling (inference.h:14-43, 80-84)
+# ---------------------------------------------------------------------------
+def sample(g, x, top_k, temperature, seed=0, counter=0, uniforms=None, eos=0, resample=False,
+           max_draws=1):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, V = (1, x.size) if x.ndim == 1 else x.shape
+    dx = g.dev(x)
+    tokens, draws = g.empty((rows,), torch.int32), g.empty((rows,), torch.int32)
+    du = g.dev_f64(uniforms) if uniforms is not None else None
+    g.call("tlh_sample_top_k", dx, rows, V, V, top_k, temperature, seed, counter, du, eos,
+           int(resample), max_draws, tokens, draws)
+    return g.host(tokens).view(np.uint32), g.host(draws).view(np.uint32)
+
+
+@pytest.mark.parametrize("rows,V,top_k,temperature", [
+    (1, 2048, 40, 0.6), (7, 2048, 5, 1.3), (3, 97, 12, 0.35), (2, 4096, 4096, 0.9),
+    (4, 300, 0, 0.5), (5, 256, 1000, 2.0), (1, 1, 1, 1.0)])
+def test_sample_top_k_matches_oracle(g, rows, V, top_k, temperature):
+    # bit-exact tokens and draw counts against the oracle on the same logits
+    # and the same SplitMix64 draws, with and without the EOS re-draw
+    x = O.normal((rows, V), 1200 + V, 0.0, 2.0)
+    for seed, counter in ((3, 0), (4, 1000)):
+        got = sample(g, x, top_k, temperature, seed, counter)
+        ref = O.sample_top_k(x, top_k, temperature, seed, counter)
+        np.testing.assert_array_equal(got[0], ref[0])
+        np.testing.assert_array_equal(got[1], ref[1])
+    eos = int(O.argmax(x[0]))  # the most likely token of row 0
+    got = sample(g, x, top_k, temperature, 5, 0, eos=eos, resample=True, max_draws=32)
+    ref = O.sample_top_k(x, top_k, temperature, 5, 0, eos=eos, resample_eos=True, max_draws=32)
+    np.testing.assert_array_equal(got[0], ref[0])
+    np.testing.assert_array_equal(got[1], ref[1])
+
+
+def test_sample_top_k_ties_nan_and_many_draws(g):
+    x = O.normal((64, 512), 1300, 0.0, 1.0)
+    x[:, 17] = x[:, 300] = x.max(axis=1) + 0.5  # ties at the top
+    x[::3, 5] = np.nan                           # NaN ranks as -INF
+    for k in (1, 2, 9):
+        got = sample(g, x, k, 0.8, seed=11)
+        ref = O.sample_top_k(x, k, 0.8, seed=11)
+        np.testing.assert_array_equal(got[0], ref[0])
+    assert np.all(sample(g, x, 1, 0.8)[0] == 17)
+    # 2000 rows of one row's logits: frequencies and the oracle, token for token
+    y = np.tile(O.normal((2048,), 1301, 0.0, 2.0), (2000, 1))
+    got = sample(g, y, 40, 0.6, seed=12)
+    np.testing.assert_array_equal(got[0], O.sample_top_k(y, 40, 0.6, seed=12)[0])
+
+
+def test_sample_top_k_reproduces_the_reference_draws(g):
+    # Fed the uniforms the reference's std::discrete_distribution drew
+    # (tests/golden/sampler_reference.json, from the reference's own
+    # inference::sample_top_k on std::mt19937), the kernel returns the
+    # reference's tokens.
+    import json
+    from pathlib import Path
+    gold = json.loads((Path(__file__).parent / "golden" / "sampler_reference.json").read_text())
+    for i, c in enumerate(gold["cases"]):
+        x = O.normal((c["vocab"],), gold["logit_seed"] + i, 0.0, 2.0)
+        u = np.array([float.fromhex(h) for h in c["uniforms"]])
+        rows = np.tile(x, (len(u), 1))
+        got = sample(g, rows, c["top_k"], c["temperature"], uniforms=u)
+        np.testing.assert_array_equal(got[0], c["tokens"], err_msg=f"case {i}")
+
+
+def test_sample_top_k_rejects_bad_arguments(g):
+    x, out = g.dev(np.zeros((2, 5000), np.float32)), g.empty((2,), torch.int32)
+    for args in ((2, 5000, 5000, 5, 1.0, 1), (2, 64, 64, 5, 0.0, 1), (2, 64, 64, 5, np.inf, 1),
+                 (2, 64, 32, 5, 1.0, 1), (2, 64, 64, 5, 1.0, 0)):
+        rows, V, stride, k, t, draws = args
+        st = g.lib.tlh_sample_top_k(x.data_ptr(), rows, V, stride, k, float(t), 0, 0, None, 0, 0,
+                                    draws, out.data_ptr(), None, g.stream)
+        assert st != 0, args
+
+
 def test_argmax_rows(g):
     x = O.normal((64, 2048), 36)
     x[3, [10, 20]] = 99.0

@@ -88,7 +88,8 @@ def test_oracle_tests_under_sanitizers():
         TEMPLIT_ORACLE_LIB=str(ORACLE_ASAN),
         TEMPLIT_REF_CPU_LIB=str(REF_ASAN if REF_ASAN.exists() else ROOT / "missing"),
     )
-    files = ["tests/test_oracle_kats.py", "tests/test_oracle_math.py"]
+    files = ["tests/test_oracle_kats.py", "tests/test_oracle_math.py",
+             "tests/test_oracle_sampler.py"]
     if REF_ASAN.exists():
         files.append("tests/test_oracle_vs_reference.py")
     proc = subprocess.run([sys.executable, "-m", "pytest", *files, "-q", "-x", "-m", "not gpu",
