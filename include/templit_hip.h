@@ -308,7 +308,8 @@ int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
  * their chunk sums are added in a fixed order (deterministic). */
 int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
 /* Tuning hook: force every following tlh_gemm / tlh_matmul to use a
- * bm x bn tile (64 or 128 each), a K tile of bk (16 or 32) and, where a
+ * bm x bn tile (64 or 128 each; or 96 x 96 with bk 32 (4 waves) or 64 (8
+ * waves)), a K tile of bk (16 or 32) and, where a
  * workspace allows it, `splits` K splits; bm = bn = 0 restores the
  * automatic plan. Process-wide, for measurement sweeps. A forced split
  * count needs a workspace sized for it (tlh_gemm_workspace_size).
@@ -317,8 +318,9 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * bk = -5 / -6 the rectangular XCD tile blocks off / on (default on),
  * bk = -7 / -8 the one-row (GEMV) path off / on (default on), bk = -9 /
  * -10 the float4 split-K reduce over a (plane, entry) grid off / on
- * (default on; off runs the grid-stride reduce, same bits); these leave
- * the plan alone. */
+ * (default on; off runs the grid-stride reduce, same bits), bk = -11 /
+ * -12 the planner's 96x96 tiles off / on (default on); these leave the
+ * plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

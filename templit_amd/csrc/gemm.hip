@@ -107,19 +107,22 @@ struct BlockCtx {
   float *C;
   const float *bias;
   float *bias_grad;
+  int bz; // the block's z coordinate: output entry * splits + split
 };
 
+// (bx, gx, bz): the block's x coordinate, the grid's x extent and its z
+// coordinate (blockIdx.x, gridDim.x, blockIdx.z of the launch).
 template <int BM, int BN>
-__device__ inline BlockCtx block_ctx(const GemmParams &p) {
+__device__ inline BlockCtx block_ctx(const GemmParams &p, int bx, int gx, int bz) {
   BlockCtx b;
   // Blocks are dispatched round-robin over the 8 XCDs (block x runs on XCD
   // x % 8), each with its own L2. Give XCD j a block of tiles that share
   // operand panels in its L2: a rectangle of the tile grid (rows share A
   // rows, columns share B columns) when the host found one that needs fewer
   // panels, else the contiguous tile range [j*G/8, (j+1)*G/8).
-  const int bx = int(blockIdx.x);
+  b.bz = bz;
   b.partial = p.tail_splits > 0 && bx >= p.dp_tiles;
-  const int nblk = p.tail_splits > 0 ? p.dp_tiles : int(gridDim.x);
+  const int nblk = p.tail_splits > 0 ? p.dp_tiles : gx;
   int tile;
   if (p.rect_m > 0) {
     const int xcd = bx & 7, i = bx >> 3, py = p.tiles_n / p.rect_n;
@@ -145,9 +148,9 @@ __device__ inline BlockCtx block_ctx(const GemmParams &p) {
   b.C = p.C;
   b.bias = p.bias;
   b.bias_grad = p.bias_grad;
-  // blockIdx.z = output entry * splits + split (a split is a K range).
-  const int zs = p.splits > 1 ? int(blockIdx.z) % p.splits : 0;
-  const int zb = p.splits > 1 ? int(blockIdx.z) / p.splits : int(blockIdx.z);
+  // bz = output entry * splits + split (a split is a K range).
+  const int zs = p.splits > 1 ? bz % p.splits : 0;
+  const int zb = p.splits > 1 ? bz / p.splits : bz;
   b.k_begin = 0;
   b.k_end = p.K;
   if (p.batch_ndim > 0) {
@@ -195,7 +198,7 @@ __device__ inline void bias_grad_store(const GemmParams &p, const BlockCtx &b, f
 #pragma unroll
     for (int g = 0; g < BGROUPS; ++g) t += smem[g * BN + tid];
     if (p.splits > 1) {
-      p.workspace[size_t(p.batch) * p.splits * p.M * p.N + size_t(blockIdx.z) * p.N + n] = t;
+      p.workspace[size_t(p.batch) * p.splits * p.M * p.N + size_t(b.bz) * p.N + n] = t;
     } else {
       b.bias_grad[n] = p.beta != 0.0f ? t + p.beta * b.bias_grad[n] : t;
     }
@@ -377,8 +380,16 @@ __device__ inline void stage_operands(float *as, float *bs, const f4 (&ra)[BM * 
 
 // FULL: M, N are multiples of the tile, the K range of every block is a
 // multiple of BK and the operands are float4-aligned: no bounds checks.
+// LDS floats of gemm_tile32: two stages of both operand tiles.
+template <int BM, int BN, int BK, bool TA, bool TB>
+constexpr int tile32_smem() {
+  constexpr int A_LD = TA ? (BM + kPad) : (BK + kPad);
+  constexpr int B_LD = TB ? (BK + kPad) : (BN + kPad);
+  return 2 * ((TA ? BK * A_LD : BM * A_LD) + (TB ? BN * B_LD : BK * B_LD));
+}
+
 template <int BM, int BN, int WM, int WN, int BK, bool TA, bool TB, bool VEC, bool FULL>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+__device__ inline void gemm_tile32(const GemmParams &p, float *smem, int bx, int gx, int bz) {
   static_assert(BK % 8 == 0 && BK <= kBK, "K tile must be a multiple of 8 and divide the split chunk");
   constexpr int TM = WM / 32;
   constexpr int TN = WN / 32;
@@ -393,8 +404,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   constexpr int A_CHUNKS = BM * BK / 4 / 256;
   constexpr int B_CHUNKS = BN * BK / 4 / 256;
   static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
-
-  __shared__ __attribute__((aligned(16))) float smem[2 * (A_TILE + B_TILE)];
+  static_assert(2 * (A_TILE + B_TILE) == tile32_smem<BM, BN, BK, TA, TB>(), "LDS geometry");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -404,7 +414,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int r = lane & 31;
   const int hk = lane >> 5;
 
-  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const BlockCtx ctx = block_ctx<BM, BN>(p, bx, gx, bz);
   const int tm = ctx.tm, m0 = ctx.m0, n0 = ctx.n0;
   const int k_begin = ctx.k_begin, k_end = ctx.k_end;
   const float *A = ctx.A;
@@ -510,6 +520,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   store_acc<BN, TM, TN, WM, WN, FULL>(p, ctx, acc, wm, wn, r, hk);
 }
 
+template <int BM, int BN, int WM, int WN, int BK, bool TA, bool TB, bool VEC, bool FULL>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) float smem[tile32_smem<BM, BN, BK, TA, TB>()];
+  gemm_tile32<BM, BN, WM, WN, BK, TA, TB, VEC, FULL>(p, smem, int(blockIdx.x), int(gridDim.x),
+                                                     int(blockIdx.z));
+}
+
 // ---- 16x16x4 MFMA tiles --------------------------------------------------------
 // v_mfma_f32_16x16x4f32 (64 lanes): lane l supplies A[m = l%16][k = l/16] and
 // B[k = l/16][n = l%16]; accumulator v of lane l holds D[4*(l/16) + v][l%16].
@@ -607,8 +624,16 @@ __device__ inline void tile_epilogue(const GemmParams &p, const BlockCtx &b, con
 // (measured: no bank conflicts; with a stride of BK + 4, or consecutive k
 // blocks per lane group, 13% of the read cycles conflict). Same staging, K loop and epilogues as gemm_mfma_kernel; no
 // bias gradient (the planner keeps those on gemm_mfma_kernel).
+// LDS floats of gemm_tile16: two stages of both operand tiles.
+template <int BM, int BN, int BK, bool TA, bool TB>
+constexpr int tile16_smem() {
+  constexpr int A_LD = TA ? (BM + kPad) : (BK + kPad16);
+  constexpr int B_LD = TB ? (BK + kPad16) : (BN + kPad);
+  return 2 * ((TA ? BK * A_LD : BM * A_LD) + (TB ? BN * B_LD : BK * B_LD));
+}
+
 template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL>
-__global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
+__device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int gx, int bz) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 16, TN = WN / 16;
   static_assert(WM % 16 == 0 && WN % 16 == 0 && BK % 16 == 0 && BK <= kBK, "tile geometry");
@@ -619,8 +644,7 @@ __global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
   constexpr int A_CHUNKS = BM * BK / 1024, B_CHUNKS = BN * BK / 1024;
   static_assert(A_CHUNKS * 1024 == BM * BK && B_CHUNKS * 1024 == BN * BK,
                 "every thread stages whole float4s of both operands");
-
-  __shared__ __attribute__((aligned(16))) float smem[2 * (A_TILE + B_TILE)];
+  static_assert(2 * (A_TILE + B_TILE) == tile16_smem<BM, BN, BK, TA, TB>(), "LDS geometry");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -628,7 +652,7 @@ __global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int r16 = lane & 15, g = lane >> 4;
 
-  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const BlockCtx ctx = block_ctx<BM, BN>(p, bx, gx, bz);
   const int m0 = ctx.m0, n0 = ctx.n0;
   const int k_begin = ctx.k_begin, k_end = ctx.k_end;
   const float *A = ctx.A;
@@ -724,6 +748,13 @@ __global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
   tile_epilogue<BM, BN, FULL>(p, ctx, ct);
 }
 
+template <int BM, int BN, int BK, bool TA, bool TB, bool VEC, bool FULL>
+__global__ __launch_bounds__(256) void gemm_mfma16_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) float smem[tile16_smem<BM, BN, BK, TA, TB>()];
+  gemm_tile16<BM, BN, BK, TA, TB, VEC, FULL>(p, smem, int(blockIdx.x), int(gridDim.x),
+                                             int(blockIdx.z));
+}
+
 // 8 waves, 2 per SIMD, in two groups of 4. Each stage holds a K tile of 64
 // of both operands (staged by all 512 threads); group h multiplies k in
 // [32h, 32h + 32) of it into its own accumulators, as gemm_mfma16_kernel's
@@ -757,7 +788,7 @@ __global__ __launch_bounds__(512) void gemm_mfma16x8_kernel(GemmParams p) {
   const int wm = wq >> 1, wn = wq & 1;
   const int r16 = lane & 15, g = lane >> 4;
 
-  const BlockCtx ctx = block_ctx<BM, BN>(p);
+  const BlockCtx ctx = block_ctx<BM, BN>(p, int(blockIdx.x), int(gridDim.x), int(blockIdx.z));
   const int m0 = ctx.m0, n0 = ctx.n0;
   const int k_begin = ctx.k_begin, k_end = ctx.k_end;
   const float *A = ctx.A;
@@ -1367,16 +1398,35 @@ size_t gemm_workspace_elems(const GemmDesc &d) {
   return tail_split(d, plan, folded_k(d)).elems(plan); // [tails, splits, bm*bn]
 }
 
-int gemm_launch(const GemmDesc &d, void *stream) {
-  if (d.M <= 0 || d.N <= 0) return 0;
+// A product planned for launch: its kernel parameters, tile plan, grid and
+// the finishing pass it needs (gemm_prepare / gemm_main / gemm_finish).
+struct Prepared {
+  bool none = false; // nothing to launch (empty output or empty batch)
+  bool gemv = false;
+  GemvPlan gv;
+  GemmParams p{};
+  Plan plan;
+  TailSplit ts;
+  dim3 grid;
+  bool ta = false, tb = false, vec = false, full = false;
+  bool k_empty = false; // K == 0: the reducer writes the epilogue of 0
+  size_t reduce_elems = 0;
+  bool v4 = false; // float4 split-K reduction
+};
+
+int gemm_prepare(const GemmDesc &d, Prepared &L) {
+  L = Prepared{};
+  if (d.M <= 0 || d.N <= 0) {
+    L.none = true;
+    return 0;
+  }
   if (d.bias_grad && (d.batch_ndim > 1 || d.remap_h > 0 || d.sum_batches))
     return int(hipErrorInvalidValue);
   // Summed batch entries: K segments of kBK-multiple length (a K tile never
   // straddles two entries' operands).
   if (d.sum_batches && (d.batch < 2 || d.batch_ndim != 1 || d.K % kBK))
     return int(hipErrorInvalidValue);
-  hipStream_t s = as_stream(stream);
-  GemmParams p{};
+  GemmParams &p = L.p;
   p.A = d.A; p.B = d.B; p.C = d.C;
   p.bias = d.bias; p.residual = d.residual; p.aux = d.aux;
   p.workspace = d.workspace;
@@ -1415,30 +1465,28 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   }
   if (gemv_ok(d) && d.workspace && g_gemv &&
       (!d.workspace_elems || gemm_workspace_elems(d) <= d.workspace_elems)) {
-    const GemvPlan gp = gemv_plan(d);
-    dim3 grid(unsigned((d.N + 255) / 256), unsigned(gp.chunks), unsigned(p.batch));
-    gemv_partial_kernel<<<grid, 256, 0, s>>>(p, gp.chunk_k, gp.chunks);
-    if (const int st = launch_status()) return st;
-    gemv_reduce_kernel<<<dim3(unsigned((d.N + 63) / 64), unsigned(p.batch)), 256, 0, s>>>(
-        p, gp.chunks);
-    return launch_status();
+    L.gemv = true;
+    L.gv = gemv_plan(d);
+    return 0;
   }
   Plan plan = make_plan(d, d.workspace != nullptr);
   if (plan.splits > 1 && d.workspace_elems && gemm_workspace_elems(d) > d.workspace_elems)
     plan = make_plan(d, false); // the given workspace is too small to split K
+  L.plan = plan;
   p.tiles_n = (d.N + plan.bn - 1) / plan.bn;
   p.xcd_remap = g_xcd_remap;
   const int tiles_m = (d.M + plan.bm - 1) / plan.bm;
   p.splits = plan.splits;
   p.k_chunk = p.splits > 1 ? ((K + p.splits - 1) / p.splits + kBK - 1) / kBK * kBK : K;
   if (p.splits > 1) p.splits = (K + p.k_chunk - 1) / p.k_chunk; // <= plan.splits
-  const size_t reduce_elems = size_t(d.M) * d.N;
-  const bool vec = vec_ok(d);
+  L.reduce_elems = size_t(d.M) * d.N;
+  L.vec = vec_ok(d);
   TailSplit ts;
-  if (p.splits <= 1 && d.workspace && vec) {
+  if (p.splits <= 1 && d.workspace && L.vec) {
     ts = tail_split(d, plan, K);
     if (ts.splits && d.workspace_elems && d.workspace_elems < ts.elems(plan)) ts = TailSplit{};
   }
+  L.ts = ts;
   p.dp_tiles = ts.dp_tiles;
   p.tail_tiles = ts.tails;
   p.tail_splits = ts.splits;
@@ -1451,17 +1499,36 @@ int gemm_launch(const GemmDesc &d, void *stream) {
   }
   if (K <= 0) { // nothing to accumulate: the reducer applies the epilogue to 0
     p.splits = 0;
-    gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
-    return launch_status();
+    L.k_empty = true;
+    return 0;
   }
   const int z = p.splits > 1 ? p.batch * p.splits : p.batch;
   const int blocks = ts.splits ? ts.dp_tiles + ts.tails * ts.splits : tiles_m * p.tiles_n;
-  dim3 grid(unsigned(blocks), 1, unsigned(z));
-  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+  L.grid = dim3(unsigned(blocks), 1, unsigned(z));
+  L.ta = d.trans_a != 0;
+  L.tb = d.trans_b != 0;
   // Every block's K range is a multiple of the K tile when K is and the
   // split chunk (a multiple of kBK) is.
-  const bool full = vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && K % plan.bk == 0 &&
-                    (p.splits <= 1 || p.k_chunk % plan.bk == 0);
+  L.full = L.vec && d.M % plan.bm == 0 && d.N % plan.bn == 0 && K % plan.bk == 0 &&
+           (p.splits <= 1 || p.k_chunk % plan.bk == 0);
+  // The workspace planes start 16-byte aligned when M*N is a multiple of 4.
+  L.v4 = d.N % 4 == 0 && (reinterpret_cast<uintptr_t>(d.workspace) & 15) == 0;
+  return 0;
+}
+
+// The product's tile (or GEMV partial) kernel.
+int gemm_main(const Prepared &L, hipStream_t s) {
+  if (L.none) return 0;
+  const GemmParams &p = L.p;
+  if (L.gemv) {
+    dim3 grid(unsigned((p.N + 255) / 256), unsigned(L.gv.chunks), unsigned(p.batch));
+    gemv_partial_kernel<<<grid, 256, 0, s>>>(p, L.gv.chunk_k, L.gv.chunks);
+    return launch_status();
+  }
+  if (L.k_empty) return 0;
+  const Plan &plan = L.plan;
+  const bool ta = L.ta, tb = L.tb, vec = L.vec, full = L.full;
+  const dim3 grid = L.grid;
   if (plan.bm == 96 && plan.bk == 64) {
     launch16x8<96, 96>(p, ta, tb, vec, full, grid, s);
   } else if (plan.bm == 96) {
@@ -1477,10 +1544,26 @@ int gemm_launch(const GemmDesc &d, void *stream) {
     else if (plan.bm == 64 && plan.bn == 128) launch_cfg<64, 128, 32, 64, 16>(p, ta, tb, vec, full, grid, s);
     else launch_cfg<64, 64, 32, 32, 16>(p, ta, tb, vec, full, grid, s);
   }
-  int st = launch_status();
-  if (st) return st;
-  if (ts.splits) {
-    const size_t groups = size_t(ts.tails) * plan.bm * plan.bn / 4;
+  return launch_status();
+}
+
+// The product's finishing pass: GEMV chunk sums, tail-tile or split-K
+// reduction (with the epilogue), or the epilogue of an empty K range.
+int gemm_finish(const Prepared &L, hipStream_t s) {
+  if (L.none) return 0;
+  const GemmParams &p = L.p;
+  if (L.gemv) {
+    gemv_reduce_kernel<<<dim3(unsigned((p.N + 63) / 64), unsigned(p.batch)), 256, 0, s>>>(
+        p, L.gv.chunks);
+    return launch_status();
+  }
+  if (L.k_empty) {
+    gemm_splitk_reduce<false><<<stride_grid(L.reduce_elems, 256), 256, 0, s>>>(p);
+    return launch_status();
+  }
+  const Plan &plan = L.plan;
+  if (L.ts.splits) {
+    const size_t groups = size_t(L.ts.tails) * plan.bm * plan.bn / 4;
     const unsigned g = stride_grid(groups, 256);
     if (plan.bm == 128 && plan.bn == 128) gemm_tail_reduce<128, 128><<<g, 256, 0, s>>>(p);
     else if (plan.bm == 128) gemm_tail_reduce<128, 64><<<g, 256, 0, s>>>(p);
@@ -1489,19 +1572,27 @@ int gemm_launch(const GemmDesc &d, void *stream) {
     return launch_status();
   }
   if (p.splits > 1) {
-    // The workspace planes start 16-byte aligned when M*N is a multiple of 4.
-    const bool v4 = d.N % 4 == 0 && (reinterpret_cast<uintptr_t>(d.workspace) & 15) == 0;
-    if (v4 && p.splits <= kMaxSplits && p.batch <= 65535 && g_reduce4)
-      gemm_splitk_reduce4<<<dim3(unsigned((std::max(reduce_elems / 4, size_t(d.N)) + 255) / 256),
+    const size_t reduce_elems = L.reduce_elems;
+    if (L.v4 && p.splits <= kMaxSplits && p.batch <= 65535 && g_reduce4)
+      gemm_splitk_reduce4<<<dim3(unsigned((std::max(reduce_elems / 4, size_t(p.N)) + 255) / 256),
                                  unsigned(p.batch)),
                             256, 0, s>>>(p);
-    else if (v4)
+    else if (L.v4)
       gemm_splitk_reduce<true><<<stride_grid(reduce_elems / 4 + 1, 256), 256, 0, s>>>(p);
     else
       gemm_splitk_reduce<false><<<stride_grid(reduce_elems, 256), 256, 0, s>>>(p);
-    st = launch_status();
+    return launch_status();
   }
-  return st;
+  return 0;
+}
+
+int gemm_launch(const GemmDesc &d, void *stream) {
+  Prepared L;
+  int st = gemm_prepare(d, L);
+  if (st) return st;
+  hipStream_t s = as_stream(stream);
+  if ((st = gemm_main(L, s))) return st;
+  return gemm_finish(L, s);
 }
 
 } // namespace tlh
@@ -1579,18 +1670,26 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   return 0;
 }
 
-TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
-  if (!desc) return int(hipErrorInvalidValue);
-  tlh::GemmDesc d = from_c(*desc);
+namespace {
+// The descriptor checks of tlh_gemm (0 or hipErrorInvalidValue).
+int check_desc(const tlh_gemm_desc &c, const tlh::GemmDesc &d) {
   if (d.M < 0 || d.N < 0 || d.K < 0) return int(hipErrorInvalidValue);
   if ((d.epilogue == tlh::kEpiGelu || d.epilogue == tlh::kEpiGeluBwd) && !d.aux)
     return int(hipErrorInvalidValue);
   if (d.remap_h > 0 && (d.remap_t <= 0 || d.remap_d <= 0 ||
                         (d.M % d.remap_t && d.M > d.remap_t) || d.N != d.remap_h * d.remap_d))
     return int(hipErrorInvalidValue);
-  if (desc->batch > 1 && (d.aux || d.epilogue != tlh::kEpiStore ||
-                          (d.residual && !d.sum_batches)))
+  if (c.batch > 1 && (d.aux || d.epilogue != tlh::kEpiStore || (d.residual && !d.sum_batches)))
     return int(hipErrorInvalidValue);
+  return 0;
+}
+} // namespace
+
+TLH_API int tlh_gemm(const tlh_gemm_desc *desc, void *stream) {
+  if (!desc) return int(hipErrorInvalidValue);
+  tlh::GemmDesc d = from_c(*desc);
+  const int st = check_desc(*desc, d);
+  if (st) return st;
   return tlh::gemm_launch(d, stream);
 }
 
