@@ -319,8 +319,9 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * bk = -7 / -8 the one-row (GEMV) path off / on (default on), bk = -9 /
  * -10 the float4 split-K reduce over a (plane, entry) grid off / on
  * (default on; off runs the grid-stride reduce, same bits), bk = -11 /
- * -12 the planner's 96x96 tiles off / on (default on); these leave the
- * plan alone. */
+ * -12 the planner's 96x96 tiles off / on (default on), bk = -13 / -14 the
+ * split-major XCD order of split-K and batched grids off / on (default on;
+ * same bits); these leave the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

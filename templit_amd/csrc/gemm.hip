@@ -55,6 +55,11 @@ struct GemmParams {
   // ((j / py) * rect_m, (j % py) * rect_n), py = tiles_n / rect_n; 8 blocks
   // tile the grid exactly. Set only without a tail split.
   int rect_m, rect_n;
+  // Split-major XCD order (0 = off, else the grid's z extent): work item
+  // w = z * gx + x, XCD j takes items [j * G/8, (j+1) * G/8) of the G = gx *
+  // gz blocks, so each XCD holds whole K splits (or batch entries) and its
+  // L2 fetches their operand panels once. Set when G is a multiple of 8.
+  int zmajor;
   uint32_t bias_bstride; // bias (and bias-gradient) elements between batch entries
   int batch;             // output entries (blockIdx.z = entry * splits + split)
   // K-segmented operands (summed batch entries): K index k lies in segment
@@ -120,6 +125,13 @@ __device__ inline BlockCtx block_ctx(const GemmParams &p, int bx, int gx, int bz
   // operand panels in its L2: a rectangle of the tile grid (rows share A
   // rows, columns share B columns) when the host found one that needs fewer
   // panels, else the contiguous tile range [j*G/8, (j+1)*G/8).
+  if (p.zmajor > 0) {
+    // the hardware puts linear block L = x + gx * z on XCD L % 8
+    const int lin = bx + gx * bz, per = (gx * p.zmajor) >> 3;
+    const int w = (lin & 7) * per + (lin >> 3);
+    bz = w / gx;
+    bx = w - bz * gx;
+  }
   b.bz = bz;
   b.partial = p.tail_splits > 0 && bx >= p.dp_tiles;
   const int nblk = p.tail_splits > 0 ? p.dp_tiles : gx;
@@ -1211,6 +1223,7 @@ XcdRect xcd_rect(int tiles_m, int tiles_n) {
 }
 int g_tail_split = 1;
 int g_tile96 = 1; // 96x96 tiles for tile-aligned products (see make_plan)
+int g_xcd_zmajor = 1; // split-major XCD order of split-K / batched grids
 constexpr int kMinSplitK = 256;    // K elements per split-K chunk, at least
 
 bool vec_ok(const GemmDesc &d) {
@@ -1492,7 +1505,15 @@ int gemm_prepare(const GemmDesc &d, Prepared &L) {
   p.tail_splits = ts.splits;
   p.tail_k_chunk = ts.k_chunk;
   p.rect_m = p.rect_n = 0;
-  if (p.xcd_remap && g_xcd_rects && !ts.splits) {
+  p.zmajor = 0;
+  const int zext = p.splits > 1 ? p.batch * p.splits : p.batch;
+  if (p.xcd_remap && g_xcd_zmajor && zext > 1 && !ts.splits &&
+      (size_t(tiles_m) * p.tiles_n * zext) % 8 == 0) {
+    // whole K splits / batch entries per XCD; the tiles of one go in row-
+    // major order to consecutive blocks of that XCD
+    p.zmajor = zext;
+    p.xcd_remap = 0;
+  } else if (p.xcd_remap && g_xcd_rects && !ts.splits) {
     const XcdRect r = xcd_rect(tiles_m, p.tiles_n);
     p.rect_m = r.rect_m;
     p.rect_n = r.rect_n;
@@ -1634,7 +1655,8 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   // bk < 0 toggles instead: the XCD-aware block order off (-1) or on (-2),
   // the tail split off (-3) or on (-4), the XCD rectangles off (-5) or on
   // (-6), the one-row GEMV off (-7) or on (-8), the float4 split-K reduction
-  // off (-9) or on (-10), the planner's 96x96 tiles off (-11) or on (-12).
+  // off (-9) or on (-10), the planner's 96x96 tiles off (-11) or on (-12),
+  // the split-major XCD order off (-13) or on (-14).
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
     return 0;
@@ -1657,6 +1679,10 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   }
   if (bk == -11 || bk == -12) {
     tlh::g_tile96 = bk == -12;
+    return 0;
+  }
+  if (bk == -13 || bk == -14) {
+    tlh::g_xcd_zmajor = bk == -14;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || (bm == 96 && bn == 96 && (bk == 32 || bk == 64)) ||

@@ -340,6 +340,7 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -8), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -10), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -12), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -14), "set_plan")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
@@ -387,6 +388,36 @@ def test_gemm_xcd_rectangles(g, forced_plan, M, N, K, ta):
         outs.append(out)
     np.testing.assert_array_equal(outs[0], outs[1])
     assert_rel(outs[0].reshape(M, N), O.matmul(a.T if ta else a, b), 1e-3, "gemm")
+
+
+@pytest.mark.parametrize("M,N,batch", [(384, 384, 1), (1536, 384, 1), (384, 2048, 1),
+                                         (384, 384, 3)])
+def test_gemm_split_major_xcd_order(g, forced_plan, M, N, batch):
+    # Split-K weight gradients (K = 6144; three entries for the batched
+    # Q/K/V form): the split-major XCD order changes which block computes a
+    # (tile, split), not how: weights and bias gradients are bitwise equal
+    # with the order off, and match the oracle.
+    K = 6144
+    x = O.normal((K, M), 42, 0, 0.5)
+    dys = O.normal((batch, K, N), 43, 0, 0.5)
+    gap = M * N + N + 64
+    outs = []
+    for toggle in (-14, -13):
+        forced_plan(0, 0, 0, toggle)
+        keep = []
+        dx_, ddy, dout = g.dev(x), g.dev(dys), g.zeros((batch * gap,))
+        d = _batched_desc(dx_, ddy, dout, True, False, M, N, K, batch, 0, K * N, gap)
+        d.bias_grad = dout.data_ptr() + 4 * M * N
+        d.bias_batch_stride = gap
+        _with_workspace(g, keep, d)
+        g.call("tlh_gemm", ctypes.byref(d))
+        outs.append(g.host(dout))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    for j in range(batch):
+        w = outs[0][j * gap:j * gap + M * N].reshape(M, N)
+        assert_rel(w, O.matmul(x.T, dys[j]), 1e-3, f"dW[{j}]")
+        bg = outs[0][j * gap + M * N:j * gap + M * N + N]
+        assert_close(bg, O.sum_to_shape(dys[j], [N]), rtol=1e-4, atol=1e-3, what=f"db[{j}]")
 
 
 @pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
