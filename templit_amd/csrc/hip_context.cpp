@@ -119,6 +119,7 @@ void init(int device) {
 }
 
 void shutdown() {
+  detail::drop_deferred_views(); // their tensors release blocks into the pool
   std::lock_guard<std::mutex> lock(g_init_mu);
   if (!g_ctx) return;
   Context &c = *g_ctx;
@@ -162,6 +163,20 @@ void check(int code, const char *what) {
   if (code != 0)
     throw std::runtime_error(std::string(what) + " failed: " + tlh_error_string(code) + " (" +
                              std::to_string(code) + ")");
+}
+
+namespace {
+AccessHook g_access_hook = nullptr;
+} // namespace
+
+void set_access_hook(AccessHook hook) noexcept { g_access_hook = hook; }
+
+void before_access(const void *base, int kind) {
+  if (g_access_hook && base) g_access_hook(base, kind);
+}
+
+void drop_deferred_views() {
+  if (g_access_hook) g_access_hook(nullptr, kAccessShutdown);
 }
 
 bool capturing() {

@@ -47,16 +47,146 @@ enum Op : uint32_t {
   kSoftmaxDerivative, kGeluBackward, kRmsNormDerivative, kAttention, kAttentionBackward,
 };
 
+void check(int code, const char *what) { detail::check(code, what); }
+
+// ---- views materialised on demand -------------------------------------------
+// The reference executor transposes an operand into a fresh destination and
+// hands it straight to one matrix product (MULT_LHS/RHS_DERIVATIVE,
+// include/passes/execute.h:187-232), and copies a gradient's first
+// contribution into its slot (context.h:73-89). Such a destination is kept
+// as a view of its source -- the source tensor (held alive), the
+// destination's shape and the source's element strides per destination dim
+// -- and filled by one transpose or copy kernel only when its bytes are
+// needed: when an op other than mult and the broadcast binary ops (which
+// read strided operands) reads it, when the destination or the source is
+// written, or on host access (the Storage hook). Either way the consuming
+// kernels see the same values.
+struct PendingView {
+  Tensor source;
+  shape_type shape, strides;
+};
+
+// Keyed by the destination's storage block. Never destroyed: views still
+// pending at exit hold device memory the context may already have released.
+std::unordered_map<const void *, PendingView> &pending_views() {
+  static auto *views = new std::unordered_map<const void *, PendingView>();
+  return *views;
+}
+
+bool contiguous(std::span<const uint32_t> shape, std::span<const uint32_t> strides) {
+  uint64_t expect = 1;
+  for (size_t i = shape.size(); i-- > 0;) {
+    if (shape[i] != 1 && strides[i] != expect) return false;
+    expect *= shape[i];
+  }
+  return true;
+}
+
+void materialise(const void *base) {
+  auto &views = pending_views();
+  const auto it = views.find(base);
+  if (it == views.end()) return;
+  PendingView v = std::move(it->second); // (its source may be released on return)
+  views.erase(it);
+  float *dst = static_cast<float *>(const_cast<void *>(base));
+  const float *src = v.source.get_storage()->data();
+  size_t n = 1;
+  for (const uint32_t d : v.shape) n *= d;
+  if (n == 0) return;
+  if (contiguous(v.shape, v.strides))
+    check(tlh_copy(src, dst, n, stream()), "materialise copy");
+  else
+    check(tlh_transpose(src, dst, uint32_t(v.shape.size()), v.shape.data(), v.strides.data(),
+                        stream()),
+          "materialise transpose");
+}
+
+// Before a kernel or the host reads block `base`.
+void reading(const void *base) {
+  if (!pending_views().empty()) materialise(base);
+}
+
+// Before a kernel or the host writes block `base`: its own pending view
+// first (partial and in-place writes keep the rest), then every view whose
+// source is this block, which needs its current contents.
+void writing(const void *base) {
+  auto &views = pending_views();
+  if (views.empty()) return;
+  materialise(base);
+  std::vector<const void *> readers;
+  for (const auto &[dst, v] : views)
+    if (v.source.get_storage()->data() == base) readers.push_back(dst);
+  for (const void *dst : readers) materialise(dst);
+}
+
+void storage_hook(const void *base, int kind) {
+  if (kind == detail::kAccessShutdown) { // the context goes: drop every view
+    auto dead = std::move(pending_views());
+    pending_views().clear();
+    return;
+  }
+  if (kind == detail::kAccessRelease) {
+    auto &views = pending_views();
+    const auto it = views.find(base);
+    if (it == views.end()) return;
+    PendingView dead = std::move(it->second); // destroyed after the erase
+    views.erase(it);
+    return;
+  }
+  if (kind == detail::kAccessRead) reading(base);
+  else writing(base);
+}
+
 template <typename T> const T *in(const RTensor<HIP, T> &t) {
   if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
-  return t.get_storage()->data();
+  const T *p = t.get_storage()->data();
+  if constexpr (std::is_same_v<T, float>) reading(p);
+  return p;
 }
 template <typename T> T *out(RTensor<HIP, T> &t) {
   if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
-  return t.get_storage()->data();
+  T *p = t.get_storage()->data();
+  if constexpr (std::is_same_v<T, float>) writing(p);
+  return p;
 }
 
-void check(int code, const char *what) { detail::check(code, what); }
+// `o` becomes a view of `a` with element strides `strides` (per dim of o):
+// o's previous contents are dead (a pending view of it is dropped), views
+// reading o are filled first, and a pending `a` is filled now.
+void defer_view(const Tensor &a, Tensor &o, shape_type strides) {
+  const float *src = in(a);
+  if (!o.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
+  const void *dst = o.get_storage()->data();
+  auto &views = pending_views();
+  if (const auto it = views.find(dst); it != views.end()) {
+    PendingView dead = std::move(it->second);
+    views.erase(it);
+  }
+  writing(dst);
+  if (src == dst) throw std::invalid_argument("view of a tensor into its own storage");
+  views[dst] = PendingView{a, o.shape(), std::move(strides)};
+}
+
+// An operand read through its strides: a pending view reads its source
+// (when `unit_inner`, only if one of the last two strides is 1, as the
+// GEMM needs); anything else is materialised.
+struct Operand {
+  const float *ptr;
+  shape_type strides;
+};
+Operand operand(const Tensor &t, bool unit_inner) {
+  auto &views = pending_views();
+  if (!views.empty() && t.get_storage()) {
+    const auto it = views.find(t.get_storage()->data());
+    if (it != views.end() && it->second.shape == t.shape()) {
+      const shape_type &st = it->second.strides;
+      const size_t r = st.size();
+      if (!unit_inner || (r >= 2 && (st[r - 1] == 1 || st[r - 2] == 1)))
+        return {it->second.source.get_storage()->data(), st};
+    }
+  }
+  return {in(t), t.strides()};
+}
 
 // Element strides of `shape`/`strides` right-aligned to `out_shape`, 0 on
 // broadcast dims (runtime.cpp:18-39).
@@ -141,6 +271,7 @@ struct Runtime::State {
 
 Runtime::Runtime() : state_(std::make_unique<State>()) {
   if (!initialised()) throw std::logic_error("HIP must be initialised before Runtime");
+  detail::set_access_hook(&storage_hook);
 }
 
 Runtime::~Runtime() { cleanup(); }
@@ -279,10 +410,37 @@ Runtime::GraphStats Runtime::graph_stats() const { return state_->stats; }
 
 namespace {
 void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn, const char *what) {
-  const auto sa = broadcast_strides(a.shape(), a.strides(), o.shape());
-  const auto sb = broadcast_strides(b.shape(), b.strides(), o.shape());
+  broadcast_strides(a.shape(), a.strides(), o.shape()); // shape checks first
+  broadcast_strides(b.shape(), b.strides(), o.shape());
   if (o.numel() == 0) return;
-  check(fn(in(a), in(b), out(o), uint32_t(o.shape().size()), o.shape().data(), sa.data(),
+  // An in-place op on a destination that is still a view (a gradient slot
+  // holding a copy of its first contribution, then add(slot, g, slot),
+  // context.h:73-89): the op writes every element of o, so the inputs that
+  // are o read the view's source and the copy is never made. (No view ever
+  // reads a block that is itself a pending view.)
+  auto &views = pending_views();
+  const void *ob_ = o.get_storage() ? static_cast<const void *>(o.get_storage()->data()) : nullptr;
+  const auto self = ob_ ? views.find(ob_) : views.end();
+  const bool same_a = a.get_storage() == o.get_storage(), same_b = b.get_storage() == o.get_storage();
+  if (self != views.end() && (same_a || same_b) && (!same_a || a.shape() == o.shape()) &&
+      (!same_b || b.shape() == o.shape())) {
+    PendingView v = std::move(self->second); // holds the source until the launch
+    views.erase(self);
+    const Operand src{v.source.get_storage()->data(), v.strides};
+    const Operand oa = same_a ? src : operand(a, false), ob = same_b ? src : operand(b, false);
+    const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
+    const auto sb = broadcast_strides(b.shape(), ob.strides, o.shape());
+    check(fn(oa.ptr, ob.ptr, o.get_storage()->data(), uint32_t(o.shape().size()),
+             o.shape().data(), sa.data(), sb.data(), stream()),
+          what);
+    return;
+  }
+  // the destination first: views of it are filled before it is written
+  float *dst = out(o);
+  const Operand oa = operand(a, false), ob = operand(b, false);
+  const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
+  const auto sb = broadcast_strides(b.shape(), ob.strides, o.shape());
+  check(fn(oa.ptr, ob.ptr, dst, uint32_t(o.shape().size()), o.shape().data(), sa.data(),
            sb.data(), stream()),
         what);
 }
@@ -366,8 +524,10 @@ void Runtime::copy(const Tensor &a, Tensor &o) {
   require_recording("copy");
   if (a.shape() != o.shape()) throw std::invalid_argument("copy destination has incorrect shape");
   note(kCopy, o.shape());
-  if (o.numel() == 0 || in(a) == out(o)) return;
-  check(tlh_copy(in(a), out(o), o.numel(), stream()), "copy");
+  if (o.numel() == 0 || a.get_storage() == o.get_storage()) return;
+  // kept as a view of `a` (contiguous, like o) until something needs o's
+  // bytes (see defer_view)
+  defer_view(a, o, o.strides());
 }
 
 // sub then in-place hadamard (runtime.cpp:843-848).
@@ -400,19 +560,34 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
     check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "mult");
     return;
   }
-  const uint32_t a_rs = a.strides()[ra - 2], a_cs = a.strides()[ra - 1];
-  const uint32_t b_rs = b.strides()[rb - 2], b_cs = b.strides()[rb - 1];
+  // the destination first (views of it are filled before it is written),
+  // then the operands: a pending transpose is read through its strides
+  float *dst = out(o);
+  Operand oa = operand(a, true), ob = operand(b, true);
+  Batch vb = simplify_batch(
+      out_batch,
+      broadcast_strides(std::span(a.shape()).first(ra - 2), std::span(oa.strides).first(ra - 2),
+                        out_batch),
+      broadcast_strides(std::span(b.shape()).first(rb - 2), std::span(ob.strides).first(rb - 2),
+                        out_batch),
+      std::span(o.strides()).first(ro - 2));
+  if (vb.shape.size() > 4) { // the views' batch dims do not merge: fill them
+    oa = {in(a), a.strides()};
+    ob = {in(b), b.strides()};
+    vb = batch;
+  }
+  const uint32_t a_rs = oa.strides[ra - 2], a_cs = oa.strides[ra - 1];
+  const uint32_t b_rs = ob.strides[rb - 2], b_cs = ob.strides[rb - 1];
   const uint32_t c_rs = o.strides()[ro - 2], c_cs = o.strides()[ro - 1];
-  const uint32_t nb = uint32_t(batch.shape.size());
+  const uint32_t nb = uint32_t(vb.shape.size());
   size_t ws_elems = 0;
   check(tlh_matmul_workspace_size(M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
-                                  batch.shape.data(), batch.sa.data(), batch.sb.data(),
-                                  batch.sc.data(), &ws_elems),
+                                  vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(),
+                                  &ws_elems),
         "mult");
   if (ws_elems == 0 || ws_elems > UINT32_MAX) {
-    check(tlh_matmul(in(a), in(b), out(o), M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
-                     batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
-                     stream()),
+    check(tlh_matmul(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                     vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(), stream()),
           "mult");
     return;
   }
@@ -420,13 +595,13 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
   // their next user is queued after this work, and while a graph is being
   // captured the pool holds released blocks back until the graph launches.
   Tensor partials({uint32_t(ws_elems)});
-  check(tlh_matmul_ws(in(a), in(b), out(o), M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
-                      batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
-                      out(partials), ws_elems, stream()),
+  check(tlh_matmul_ws(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                      vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(), out(partials),
+                      ws_elems, stream()),
         "mult");
 }
 
-// Materialised swap of two dims (runtime.cpp:529-569).
+// Swap of two dims (runtime.cpp:529-569): a view of `a` filled on demand.
 void Runtime::transpose(const Tensor &a, Tensor &o, int32_t dim_a, int32_t dim_b) {
   require_recording("transpose");
   if (a.shape().size() < 2) throw std::invalid_argument("transpose requires rank >= 2");
@@ -440,6 +615,11 @@ void Runtime::transpose(const Tensor &a, Tensor &o, int32_t dim_a, int32_t dim_b
   if (o.numel() == 0) return;
   shape_type strides = a.strides();
   std::swap(strides[x], strides[y]);
+  if (a.get_storage() != o.get_storage()) {
+    // kept as a strided view of `a` until something needs o's bytes
+    defer_view(a, o, std::move(strides));
+    return;
+  }
   check(tlh_transpose(in(a), out(o), uint32_t(o.shape().size()), o.shape().data(),
                       strides.data(), stream()),
         "transpose");
@@ -507,7 +687,8 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
     return;
   }
   if (!reduces) {
-    if (in(a) != out(o)) check(tlh_copy(in(a), out(o), o.numel(), stream()), "sum_to_shape");
+    // the same elements in the same order: a contiguous view of `a`
+    if (a.get_storage() != o.get_storage() && o.numel() > 0) defer_view(a, o, o.strides());
     return;
   }
   size_t ws_elems = 0;

@@ -72,6 +72,18 @@ bool equal(const void *a, const void *b, size_t bytes);
 bool capturing();
 // Throws std::runtime_error naming `what` when `code` (a hipError_t) != 0.
 void check(int code, const char *what);
+
+// Deferred device work on a storage block: hip::Runtime keeps some results
+// as views to be materialised later (a transpose or copy that only a matrix
+// product or broadcast op reads). Storage calls the installed hook with the
+// block's base pointer before host access -- kAccessRead, kAccessWrite --
+// and before releasing it (kAccessRelease, which must not throw); shutdown()
+// calls it with kAccessShutdown (and no block) before the context goes.
+enum AccessKind : int { kAccessRead = 0, kAccessWrite = 1, kAccessRelease = 2, kAccessShutdown = 3 };
+using AccessHook = void (*)(const void *base, int kind);
+void set_access_hook(AccessHook hook) noexcept;
+void before_access(const void *base, int kind);
+void drop_deferred_views();
 } // namespace detail
 
 } // namespace hip

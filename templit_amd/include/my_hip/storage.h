@@ -29,7 +29,10 @@ public:
   Storage &operator=(const Storage &) = delete;
   Storage(Storage &&) = delete;
   Storage &operator=(Storage &&) = delete;
-  ~Storage() { hip::detail::release(data_, size_ * sizeof(T)); }
+  ~Storage() {
+    hip::detail::before_access(data_, hip::detail::kAccessRelease);
+    hip::detail::release(data_, size_ * sizeof(T));
+  }
 
   int ref_count;
 
@@ -40,16 +43,21 @@ public:
 
   void write(std::span<const T> values, size_t offset) {
     if (offset + values.size() > size_) throw std::out_of_range("write out of bounds");
-    if (!values.empty()) hip::detail::write(data_ + offset, values.data(), values.size_bytes());
+    if (values.empty()) return;
+    hip::detail::before_access(data_, hip::detail::kAccessWrite);
+    hip::detail::write(data_ + offset, values.data(), values.size_bytes());
   }
 
   void read(std::span<T> out, size_t offset) const {
     if (offset + out.size() > size_) throw std::out_of_range("read out of bounds");
-    if (!out.empty()) hip::detail::read(out.data(), data_ + offset, out.size_bytes());
+    if (out.empty()) return;
+    hip::detail::before_access(data_, hip::detail::kAccessRead);
+    hip::detail::read(out.data(), data_ + offset, out.size_bytes());
   }
 
   void fill(T value) {
     if (size_ == 0) return;
+    hip::detail::before_access(data_, hip::detail::kAccessWrite);
     if constexpr (sizeof(T) == 4) {
       uint32_t pattern;
       std::memcpy(&pattern, &value, 4);
@@ -62,12 +70,18 @@ public:
 
   Storage *clone() const {
     auto *other = new Storage(size_);
-    if (size_) hip::detail::copy(other->data_, data_, size_ * sizeof(T));
+    if (size_) {
+      hip::detail::before_access(data_, hip::detail::kAccessRead);
+      hip::detail::copy(other->data_, data_, size_ * sizeof(T));
+    }
     return other;
   }
 
   bool compare(const Storage &other) const {
-    return other.size_ == size_ && hip::detail::equal(data_, other.data_, size_ * sizeof(T));
+    if (other.size_ != size_) return false;
+    hip::detail::before_access(data_, hip::detail::kAccessRead);
+    hip::detail::before_access(other.data_, hip::detail::kAccessRead);
+    return hip::detail::equal(data_, other.data_, size_ * sizeof(T));
   }
 
 private:

@@ -606,6 +606,84 @@ void graph_mode_scratch_is_not_reused_within_a_capture(hip::Runtime &rt) {
 
 // sqe = (prediction - target)^2 elementwise (runtime.cpp:843-848), with
 // the executor's broadcasting and in place.
+// transpose / copy / identity sum_to_shape results are views filled on
+// demand: every way to observe them gives the materialised values.
+void deferred_views(hip::Runtime &rt) {
+  const std::vector<float> av = random_values(6 * 4, 11), bv = random_values(6 * 5, 12);
+  Tensor a({6, 4}), b({6, 5});
+  a.set(std::span<const float>(av));
+  b.set(std::span<const float>(bv));
+  auto at = [&](size_t r, size_t c) { return av[r * 4 + c]; };
+  // 1. host read of a transpose
+  Tensor t1({4, 6});
+  run(rt, [&] { rt.transpose(a, t1); });
+  {
+    const auto got = host(t1);
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 6; ++j) CHECK(got[i * 6 + j] == at(j, i));
+  }
+  // 2. the transposed operand of a product (read through its strides), then
+  // the source overwritten while a second view of it is pending
+  Tensor t2({4, 6}), p({4, 5}), c({6, 4});
+  run(rt, [&] {
+    rt.transpose(a, t2);
+    rt.mult(t2, b, p);       // A^T . B
+    rt.add(a, a, a);         // the source changes: t2 must keep the old values
+  });
+  {
+    const auto got = host(p);
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 5; ++j) {
+        double e = 0;
+        for (size_t k = 0; k < 6; ++k) e += double(at(k, i)) * bv[k * 5 + j];
+        CHECK_NEAR(got[i * 5 + j], e, 1e-5);
+      }
+    const auto t2h = host(t2), ah = host(a);
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 6; ++j) {
+        CHECK(t2h[i * 6 + j] == at(j, i));
+        CHECK(ah[j * 4 + i] == at(j, i) + at(j, i));
+      }
+  }
+  a.set(std::span<const float>(av));
+  // 3. copy then in-place accumulation (GradientContext::accumulate), a host
+  // write to the source of a pending copy, and a transpose into a reused
+  // destination
+  Tensor g({6, 4}), h({6, 4}), s({6, 4}), r({4, 6});
+  run(rt, [&] {
+    rt.copy(a, g);
+    rt.add(g, a, g); // g = 2a
+    rt.copy(a, h);
+    rt.transpose(a, r);
+    rt.transpose(g, r); // r is overwritten before its first view was filled
+    rt.sum_to_shape(a, std::vector<uint32_t>{6, 4}, s);
+  });
+  std::vector<float> zeros(24, 0.0f);
+  a.set(std::span<const float>(zeros)); // the pending copy h keeps a's old values
+  {
+    const auto gh = host(g), hh = host(h), rh = host(r), sh = host(s);
+    for (size_t i = 0; i < 24; ++i) {
+      CHECK(gh[i] == av[i] + av[i]);
+      CHECK(hh[i] == av[i]);
+      CHECK(sh[i] == av[i]);
+    }
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 6; ++j) CHECK(rh[i * 6 + j] == at(j, i) + at(j, i));
+  }
+  // 4. an elementwise consumer (not a product or broadcast op) fills the view
+  Tensor e({4, 6});
+  a.set(std::span<const float>(av));
+  run(rt, [&] {
+    rt.transpose(a, t1);
+    rt.exp(t1, e);
+  });
+  {
+    const auto got = host(e);
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 6; ++j) CHECK_NEAR(got[i * 6 + j], std::exp(at(j, i)), 1e-5);
+  }
+}
+
 void sqe(hip::Runtime &rt) {
   Tensor p({2, 3}), t({2, 3}), row({3}), o({2, 3}), ob({2, 3});
   fill(p, {1, -2, 3.5f, 0, 10, -7});
@@ -706,6 +784,7 @@ int main(int argc, char **argv) {
     harness::run("graph_mode_scratch_is_not_reused_within_a_capture",
                  [&] { graph_mode_scratch_is_not_reused_within_a_capture(rt); });
     harness::run("sqe", [&] { sqe(rt); });
+    harness::run("deferred_views", [&] { deferred_views(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
