@@ -150,21 +150,72 @@ template <typename T> T *out(RTensor<HIP, T> &t) {
   return p;
 }
 
-// `o` becomes a view of `a` with element strides `strides` (per dim of o):
-// o's previous contents are dead (a pending view of it is dropped), views
-// reading o are filled first, and a pending `a` is filled now.
-void defer_view(const Tensor &a, Tensor &o, shape_type strides) {
-  const float *src = in(a);
-  if (!o.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
-  const void *dst = o.get_storage()->data();
+// Drops the pending view of block `base`, if any, without filling it.
+void drop_view(const void *base) {
   auto &views = pending_views();
-  if (const auto it = views.find(dst); it != views.end()) {
-    PendingView dead = std::move(it->second);
-    views.erase(it);
-  }
+  const auto it = views.find(base);
+  if (it == views.end()) return;
+  PendingView dead = std::move(it->second); // destroyed after the erase
+  views.erase(it);
+}
+
+// The pending view of `t` when it covers t exactly (its own shape).
+const PendingView *view_of(const Tensor &t) {
+  auto &views = pending_views();
+  if (views.empty() || !t.get_storage()) return nullptr;
+  const auto it = views.find(t.get_storage()->data());
+  return it != views.end() && it->second.shape == t.shape() ? &it->second : nullptr;
+}
+
+// `o` becomes a view of `a`, o's dim d being a's dim perm[d] (a transpose,
+// or with the identity a copy of the same shape). o's previous contents are
+// dead (a pending view of o is dropped) and views reading o are filled
+// first. A pending `a` is composed: o then views a's source.
+void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
+  if (!o.get_storage() || !a.get_storage())
+    throw std::logic_error("operation on an uninitialised tensor");
+  const void *dst = o.get_storage()->data();
+  drop_view(dst);
   writing(dst);
-  if (src == dst) throw std::invalid_argument("view of a tensor into its own storage");
-  views[dst] = PendingView{a, o.shape(), std::move(strides)};
+  shape_type strides(perm.size());
+  Tensor source = a;
+  if (const PendingView *v = view_of(a)) {
+    source = v->source;
+    for (size_t d = 0; d < perm.size(); ++d) strides[d] = v->strides[perm[d]];
+  } else {
+    in(a);
+    for (size_t d = 0; d < perm.size(); ++d) strides[d] = a.strides()[perm[d]];
+  }
+  if (source.get_storage() == o.get_storage())
+    throw std::invalid_argument("view of a tensor into its own storage");
+  pending_views()[dst] = PendingView{std::move(source), o.shape(), std::move(strides)};
+}
+
+// `o` (same element count, another shape) becomes a view of the elements
+// of `a` in order.
+void defer_reshape(const Tensor &a, Tensor &o) {
+  if (o.shape() == a.shape()) {
+    std::vector<size_t> identity(o.shape().size());
+    std::iota(identity.begin(), identity.end(), size_t(0));
+    defer_view(a, o, identity);
+    return;
+  }
+  const void *dst = o.get_storage()->data();
+  drop_view(dst);
+  writing(dst);
+  in(a);
+  pending_views()[dst] = PendingView{a, o.shape(), o.strides()};
+}
+
+// The destination of an op that writes every element of `o`: a pending view
+// of o is dropped unfilled (its bytes are dead) unless one of `inputs`
+// shares o's storage and so reads them; views reading o are filled first.
+float *dest(Tensor &o, std::initializer_list<const Tensor *> inputs) {
+  if (!o.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
+  bool read = false;
+  for (const Tensor *t : inputs) read = read || t->get_storage() == o.get_storage();
+  if (!read) drop_view(o.get_storage()->data());
+  return out(o);
 }
 
 // An operand read through its strides: a pending view reads its source
@@ -436,7 +487,7 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
     return;
   }
   // the destination first: views of it are filled before it is written
-  float *dst = out(o);
+  float *dst = dest(o, {&a, &b});
   const Operand oa = operand(a, false), ob = operand(b, false);
   const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
   const auto sb = broadcast_strides(b.shape(), ob.strides, o.shape());
@@ -448,14 +499,16 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
 void unary(const Tensor &a, Tensor &o, UnaryFn fn, const char *what) {
   require_same_count(a, o, what);
   if (o.numel() == 0) return;
-  check(fn(in(a), out(o), o.numel(), stream()), what);
+  float *dst = dest(o, {&a});
+  check(fn(in(a), dst, o.numel(), stream()), what);
 }
 
 void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *what) {
   if (a.shape() != o.shape())
     throw std::invalid_argument("scalar operation input and output shapes must match");
   if (o.numel() == 0) return;
-  check(fn(in(a), v, out(o), o.numel(), stream()), what);
+  float *dst = dest(o, {&a});
+  check(fn(in(a), v, dst, o.numel(), stream()), what);
 }
 } // namespace
 
@@ -525,9 +578,8 @@ void Runtime::copy(const Tensor &a, Tensor &o) {
   if (a.shape() != o.shape()) throw std::invalid_argument("copy destination has incorrect shape");
   note(kCopy, o.shape());
   if (o.numel() == 0 || a.get_storage() == o.get_storage()) return;
-  // kept as a view of `a` (contiguous, like o) until something needs o's
-  // bytes (see defer_view)
-  defer_view(a, o, o.strides());
+  // kept as a view of `a` until something needs o's bytes (see defer_view)
+  defer_reshape(a, o);
 }
 
 // sub then in-place hadamard (runtime.cpp:843-848).
@@ -562,7 +614,7 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
   }
   // the destination first (views of it are filled before it is written),
   // then the operands: a pending transpose is read through its strides
-  float *dst = out(o);
+  float *dst = dest(o, {&a, &b});
   Operand oa = operand(a, true), ob = operand(b, true);
   Batch vb = simplify_batch(
       out_batch,
@@ -617,7 +669,10 @@ void Runtime::transpose(const Tensor &a, Tensor &o, int32_t dim_a, int32_t dim_b
   std::swap(strides[x], strides[y]);
   if (a.get_storage() != o.get_storage()) {
     // kept as a strided view of `a` until something needs o's bytes
-    defer_view(a, o, std::move(strides));
+    std::vector<size_t> perm(a.shape().size());
+    std::iota(perm.begin(), perm.end(), size_t(0));
+    std::swap(perm[x], perm[y]);
+    defer_view(a, o, perm);
     return;
   }
   check(tlh_transpose(in(a), out(o), uint32_t(o.shape().size()), o.shape().data(),
@@ -687,8 +742,8 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
     return;
   }
   if (!reduces) {
-    // the same elements in the same order: a contiguous view of `a`
-    if (a.get_storage() != o.get_storage() && o.numel() > 0) defer_view(a, o, o.strides());
+    // the same elements in the same order: a view of `a`
+    if (a.get_storage() != o.get_storage() && o.numel() > 0) defer_reshape(a, o);
     return;
   }
   size_t ws_elems = 0;
@@ -869,7 +924,12 @@ void Runtime::accumulate_gradient_squared_norm(const Tensor &g, Tensor &s) {
   if (s.numel() != 1) throw std::invalid_argument("gradient norm destination must be a scalar");
   note(kSquaredNorm, g.shape());
   if (g.numel() == 0) return;
-  check(tlh_accumulate_gradient_squared_norm(in(g), g.numel(), out(s), stream()),
+  float *acc = out(s);
+  // a gradient slot still holding a copy of its one contribution
+  // (context.h:73-89) is read at the copy's source
+  const PendingView *v = view_of(g);
+  const float *src = v && v->strides == g.strides() ? v->source.get_storage()->data() : in(g);
+  check(tlh_accumulate_gradient_squared_norm(src, g.numel(), acc, stream()),
         "accumulate_gradient_squared_norm");
 }
 
@@ -882,7 +942,19 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
     throw std::invalid_argument("maximum gradient norm must be finite and positive");
   note(kClip, g.shape());
   if (g.numel() == 0) return;
-  check(tlh_clip_gradient(in(g), in(s), max_norm, out(o), g.numel(), stream()), "clip_gradient");
+  // in place on a slot that still holds a copy: read the copy's source and
+  // write every element of the slot, so the copy is never made
+  if (const PendingView *v = view_of(g);
+      v && v->strides == g.strides() && g.get_storage() == o.get_storage()) {
+    PendingView copy = *v; // holds the source until the launch
+    drop_view(o.get_storage()->data());
+    check(tlh_clip_gradient(copy.source.get_storage()->data(), in(s), max_norm,
+                            o.get_storage()->data(), g.numel(), stream()),
+          "clip_gradient");
+    return;
+  }
+  float *dst = dest(o, {&g, &s});
+  check(tlh_clip_gradient(in(g), in(s), max_norm, dst, g.numel(), stream()), "clip_gradient");
 }
 
 void Runtime::adamW(const Tensor &p, const Tensor &g, Tensor &o, Tensor &m1, Tensor &m2,

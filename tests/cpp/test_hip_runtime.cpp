@@ -682,6 +682,46 @@ void deferred_views(hip::Runtime &rt) {
     for (size_t i = 0; i < 4; ++i)
       for (size_t j = 0; j < 6; ++j) CHECK_NEAR(got[i * 6 + j], std::exp(at(j, i)), 1e-5);
   }
+  // 5. views of views: a transpose of a pending transpose and a copy of it
+  // view the first source; the intermediate is then overwritten whole (its
+  // view is dropped, never filled) and the source changes afterwards
+  const std::vector<float> xv = random_values(2 * 3 * 4, 13);
+  Tensor x({2, 3, 4}), x1({3, 2, 4}), x2({3, 4, 2}), x3({3, 4, 2}), y({3, 2, 4});
+  x.set(std::span<const float>(xv));
+  y.set(std::span<const float>(xv));
+  run(rt, [&] {
+    rt.transpose(x, x1, 0, 1);
+    rt.transpose(x1, x2, 1, 2);
+    rt.copy(x2, x3);
+    rt.divide(y, 0.5f, x1); // x1 = 2y: its pending view is dead
+    rt.add(x, x, x);       // x changes: x2 and x3 keep its old values
+  });
+  {
+    const auto h1 = host(x1), h2 = host(x2), h3 = host(x3), hx = host(x);
+    for (size_t i = 0; i < 2; ++i)
+      for (size_t j = 0; j < 3; ++j)
+        for (size_t k = 0; k < 4; ++k) {
+          const float v = xv[(i * 3 + j) * 4 + k];
+          CHECK(h1[(i * 3 + j) * 4 + k] == 2.0f * v); // y holds xv in the same order
+          CHECK(h2[(j * 4 + k) * 2 + i] == v);
+          CHECK(h3[(j * 4 + k) * 2 + i] == v);
+          CHECK(hx[(i * 3 + j) * 4 + k] == v + v);
+        }
+  }
+  // 6. the squared norm reads a pending copy's source, and an in-place clip
+  // of the copy writes it without the copy being made; the source keeps its
+  // values
+  Tensor gsrc({3}), gslot({3});
+  Tensor sq = Tensor::from_zeros({1});
+  fill(gsrc, {3, 4, 12});
+  run(rt, [&] {
+    rt.copy(gsrc, gslot);
+    rt.accumulate_gradient_squared_norm(gslot, sq);
+    rt.clip_gradient(gslot, sq, 1.0f, gslot);
+  });
+  expect(sq, {169});
+  expect(gslot, {3.0f / 13, 4.0f / 13, 12.0f / 13});
+  expect(gsrc, {3, 4, 12});
 }
 
 void sqe(hip::Runtime &rt) {
