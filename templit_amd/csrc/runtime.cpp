@@ -61,9 +61,22 @@ void check(int code, const char *what) { detail::check(code, what); }
 // read strided operands) reads it, when the destination or the source is
 // written, or on host access (the Storage hook). Either way the consuming
 // kernels see the same values.
+//
+// A batched product whose batch entries chain into its inner dimension
+// (MULT_RHS_DERIVATIVE's per-sequence weight gradient X_b^T . G_b, which
+// the executor then sums over the batch with sum_to_shape) is kept pending
+// the same way: sum_to_shape over exactly its batch dims runs one product
+// with the batch folded into K, and anything else that needs the bytes runs
+// the batched product.
+struct ProductPlan {
+  Tensor b;                                  // the second operand's data (held)
+  uint32_t M, K, N, a_rs, a_cs, b_rs, b_cs;  // source = the first operand's data
+  std::vector<uint32_t> batch, sa, sb, sc;   // merged batch dims
+};
 struct PendingView {
   Tensor source;
   shape_type shape, strides;
+  std::shared_ptr<const ProductPlan> product; // set: a pending product, not a view
 };
 
 // Keyed by the destination's storage block. Never destroyed: views still
@@ -93,6 +106,14 @@ void materialise(const void *base) {
   size_t n = 1;
   for (const uint32_t d : v.shape) n *= d;
   if (n == 0) return;
+  if (const ProductPlan *p = v.product.get()) {
+    const size_t r = v.shape.size();
+    check(tlh_matmul(src, p->b.get_storage()->data(), dst, p->M, p->K, p->N, p->a_rs, p->a_cs,
+                     p->b_rs, p->b_cs, v.shape[r - 1], 1, uint32_t(p->batch.size()),
+                     p->batch.data(), p->sa.data(), p->sb.data(), p->sc.data(), stream()),
+          "materialise product");
+    return;
+  }
   if (contiguous(v.shape, v.strides))
     check(tlh_copy(src, dst, n, stream()), "materialise copy");
   else
@@ -115,7 +136,9 @@ void writing(const void *base) {
   materialise(base);
   std::vector<const void *> readers;
   for (const auto &[dst, v] : views)
-    if (v.source.get_storage()->data() == base) readers.push_back(dst);
+    if (v.source.get_storage()->data() == base ||
+        (v.product && v.product->b.get_storage()->data() == base))
+      readers.push_back(dst);
   for (const void *dst : readers) materialise(dst);
 }
 
@@ -164,7 +187,9 @@ const PendingView *view_of(const Tensor &t) {
   auto &views = pending_views();
   if (views.empty() || !t.get_storage()) return nullptr;
   const auto it = views.find(t.get_storage()->data());
-  return it != views.end() && it->second.shape == t.shape() ? &it->second : nullptr;
+  return it != views.end() && it->second.shape == t.shape() && !it->second.product
+             ? &it->second
+             : nullptr;
 }
 
 // `o` becomes a view of `a`, o's dim d being a's dim perm[d] (a transpose,
@@ -224,19 +249,16 @@ float *dest(Tensor &o, std::initializer_list<const Tensor *> inputs) {
 struct Operand {
   const float *ptr;
   shape_type strides;
+  const Tensor *holder; // the tensor whose storage holds the data
 };
 Operand operand(const Tensor &t, bool unit_inner) {
-  auto &views = pending_views();
-  if (!views.empty() && t.get_storage()) {
-    const auto it = views.find(t.get_storage()->data());
-    if (it != views.end() && it->second.shape == t.shape()) {
-      const shape_type &st = it->second.strides;
-      const size_t r = st.size();
-      if (!unit_inner || (r >= 2 && (st[r - 1] == 1 || st[r - 2] == 1)))
-        return {it->second.source.get_storage()->data(), st};
-    }
+  if (const PendingView *v = view_of(t)) {
+    const shape_type &st = v->strides;
+    const size_t r = st.size();
+    if (!unit_inner || (r >= 2 && (st[r - 1] == 1 || st[r - 2] == 1)))
+      return {v->source.get_storage()->data(), st, &v->source};
   }
-  return {in(t), t.strides()};
+  return {in(t), t.strides(), &t};
 }
 
 // Element strides of `shape`/`strides` right-aligned to `out_shape`, 0 on
@@ -473,11 +495,11 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   const void *ob_ = o.get_storage() ? static_cast<const void *>(o.get_storage()->data()) : nullptr;
   const auto self = ob_ ? views.find(ob_) : views.end();
   const bool same_a = a.get_storage() == o.get_storage(), same_b = b.get_storage() == o.get_storage();
-  if (self != views.end() && (same_a || same_b) && (!same_a || a.shape() == o.shape()) &&
-      (!same_b || b.shape() == o.shape())) {
+  if (self != views.end() && !self->second.product && (same_a || same_b) &&
+      (!same_a || a.shape() == o.shape()) && (!same_b || b.shape() == o.shape())) {
     PendingView v = std::move(self->second); // holds the source until the launch
     views.erase(self);
-    const Operand src{v.source.get_storage()->data(), v.strides};
+    const Operand src{v.source.get_storage()->data(), v.strides, &v.source};
     const Operand oa = same_a ? src : operand(a, false), ob = same_b ? src : operand(b, false);
     const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
     const auto sb = broadcast_strides(b.shape(), ob.strides, o.shape());
@@ -591,6 +613,29 @@ void Runtime::sqe(const Tensor &prediction, const Tensor &target, Tensor &o) {
 // ---- products and layout ----------------------------------------------------
 
 // Batched broadcasting matmul (runtime.cpp:375-505) on the fp32 MFMA GEMM.
+namespace {
+// One (batched) product; K-chunk partials (tail split / split-K) come from
+// the pool and return to it on exit: their next user is queued after this
+// work, and while a graph is being captured the pool holds released blocks
+// back until the graph launches.
+void run_product(const float *a, const float *b, float *c, uint32_t M, uint32_t K, uint32_t N,
+                 uint32_t a_rs, uint32_t a_cs, uint32_t b_rs, uint32_t b_cs, uint32_t c_rs,
+                 uint32_t c_cs, const Batch &batch, size_t ws_elems) {
+  const uint32_t nb = uint32_t(batch.shape.size());
+  if (ws_elems == 0 || ws_elems > UINT32_MAX) {
+    check(tlh_matmul(a, b, c, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb, batch.shape.data(),
+                     batch.sa.data(), batch.sb.data(), batch.sc.data(), stream()),
+          "mult");
+    return;
+  }
+  Tensor partials({uint32_t(ws_elems)});
+  check(tlh_matmul_ws(a, b, c, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
+                      batch.shape.data(), batch.sa.data(), batch.sb.data(), batch.sc.data(),
+                      out(partials), ws_elems, stream()),
+        "mult");
+}
+} // namespace
+
 void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
   require_recording("mult");
   const shape_type expected = rtensor::infer_mult(a.shape(), b.shape());
@@ -637,20 +682,29 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
                                   vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(),
                                   &ws_elems),
         "mult");
-  if (ws_elems == 0 || ws_elems > UINT32_MAX) {
-    check(tlh_matmul(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
-                     vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(), stream()),
-          "mult");
+  // A batched product whose batch entries continue its inner dimension in
+  // both operands (entry i+1 starts where entry i's K run would go on) is
+  // kept pending: a following sum over the batch becomes one product over
+  // K * entries (see sum_to_shape). Only products that need no scratch and
+  // write a contiguous destination that no operand shares are deferred.
+  const auto chains = [&](const std::vector<uint32_t> &st, uint64_t k_stride) {
+    for (size_t i = nb; i-- > 0;) {
+      if (st[i] != k_stride) return false;
+      k_stride *= vb.shape[i];
+    }
+    return true;
+  };
+  const auto *os = o.get_storage();
+  if (nb > 0 && ws_elems == 0 && contiguous(o.shape(), o.strides()) &&
+      chains(vb.sa, uint64_t(K) * a_cs) && chains(vb.sb, uint64_t(K) * b_rs) &&
+      oa.holder->get_storage() != os && ob.holder->get_storage() != os &&
+      oa.ptr == oa.holder->get_storage()->data() && ob.ptr == ob.holder->get_storage()->data()) {
+    auto plan = std::make_shared<ProductPlan>(
+        ProductPlan{*ob.holder, M, K, N, a_rs, a_cs, b_rs, b_cs, vb.shape, vb.sa, vb.sb, vb.sc});
+    pending_views()[dst] = PendingView{*oa.holder, o.shape(), o.strides(), std::move(plan)};
     return;
   }
-  // K-chunk partials (tail split / split-K), returned to the pool on exit:
-  // their next user is queued after this work, and while a graph is being
-  // captured the pool holds released blocks back until the graph launches.
-  Tensor partials({uint32_t(ws_elems)});
-  check(tlh_matmul_ws(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, nb,
-                      vb.shape.data(), vb.sa.data(), vb.sb.data(), vb.sc.data(), out(partials),
-                      ws_elems, stream()),
-        "mult");
+  run_product(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, vb, ws_elems);
 }
 
 // Swap of two dims (runtime.cpp:529-569): a view of `a` filled on demand.
@@ -745,6 +799,34 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
     // the same elements in the same order: a view of `a`
     if (a.get_storage() != o.get_storage() && o.numel() > 0) defer_reshape(a, o);
     return;
+  }
+  // The sum over every batch dim of a pending batched product whose entries
+  // chain into K: one product over K * entries, written straight into o.
+  // `a` stays pending (its sources are unchanged).
+  if (const auto it = pending_views().find(a.get_storage()->data());
+      it != pending_views().end() && it->second.product && it->second.shape == as &&
+      a.get_storage() != o.get_storage() && it->second.source.get_storage() != o.get_storage() &&
+      it->second.product->b.get_storage() != o.get_storage()) {
+    const size_t r = as.size();
+    bool batch_only = aligned[r - 2] == as[r - 2] && aligned[r - 1] == as[r - 1];
+    for (size_t i = 0; i + 2 < r; ++i) batch_only = batch_only && aligned[i] == 1;
+    if (batch_only) {
+      const PendingView v = it->second; // holds the sources until the launch
+      const ProductPlan &p = *v.product;
+      uint64_t k = p.K;
+      for (const uint32_t d : p.batch) k *= d;
+      if (k <= UINT32_MAX) {
+        float *dst = dest(o, {&a});
+        const Batch none;
+        size_t ws_elems = 0;
+        check(tlh_matmul_workspace_size(p.M, uint32_t(k), p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs,
+                                        p.N, 1, 0, nullptr, nullptr, nullptr, nullptr, &ws_elems),
+              "sum_to_shape");
+        run_product(v.source.get_storage()->data(), p.b.get_storage()->data(), dst, p.M,
+                    uint32_t(k), p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs, p.N, 1, none, ws_elems);
+        return;
+      }
+    }
   }
   size_t ws_elems = 0;
   check(tlh_sum_to_shape_workspace(uint32_t(as.size()), as.data(), aligned.data(), &ws_elems),

@@ -724,6 +724,93 @@ void deferred_views(hip::Runtime &rt) {
   expect(gsrc, {3, 4, 12});
 }
 
+// A per-entry weight gradient as the executor forms it
+// (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
+// input, a batched product with the output gradient, then sum_to_shape over
+// the batch. The product is kept pending and the sum runs as one product
+// over K * entries; the product's own values are still there when read.
+void deferred_products(hip::Runtime &rt) {
+  constexpr uint32_t B = 3, T = 5, I = 4, O = 6;
+  const std::vector<float> xv = random_values(B * T * I, 21), gv = random_values(B * T * O, 22);
+  Tensor x({B, T, I}), g({B, T, O}), xt({B, I, T}), prod({B, I, O}), w({I, O}), w1({1, I, O});
+  x.set(std::span<const float>(xv));
+  g.set(std::span<const float>(gv));
+  auto per = [&](size_t b, size_t i, size_t o) {
+    double e = 0;
+    for (size_t t = 0; t < T; ++t) e += double(xv[(b * T + t) * I + i]) * gv[(b * T + t) * O + o];
+    return e;
+  };
+  auto check_sum = [&](const Tensor &t) {
+    const auto got = host(t);
+    for (size_t i = 0; i < I; ++i)
+      for (size_t o = 0; o < O; ++o) {
+        double e = 0;
+        for (size_t b = 0; b < B; ++b) e += per(b, i, o);
+        CHECK_NEAR(got[i * O + o], e, 1e-5);
+      }
+  };
+  // 1. summed twice (rank-dropping and rank-keeping targets), then the
+  // batched values read after the sources changed
+  Tensor zeros_x({B, T, I}), zeros_g({B, T, O});
+  zeros_x.set(std::vector<float>(B * T * I, 0.0f));
+  zeros_g.set(std::vector<float>(B * T * O, 0.0f));
+  run(rt, [&] {
+    rt.transpose(x, xt);
+    rt.mult(xt, g, prod);
+    rt.sum_to_shape(prod, std::vector<uint32_t>{I, O}, w);
+    rt.sum_to_shape(prod, std::vector<uint32_t>{1, I, O}, w1);
+    rt.copy(zeros_x, x); // the product must keep the old operands
+    rt.copy(zeros_g, g);
+  });
+  check_sum(w);
+  check_sum(w1);
+  {
+    const auto got = host(prod);
+    for (size_t b = 0; b < B; ++b)
+      for (size_t i = 0; i < I; ++i)
+        for (size_t o = 0; o < O; ++o) CHECK_NEAR(got[(b * I + i) * O + o], per(b, i, o), 1e-5);
+  }
+  // 2. a pending product read by another kernel, then overwritten whole
+  x.set(std::span<const float>(xv));
+  g.set(std::span<const float>(gv));
+  Tensor e({B, I, O}), other({B, I, O});
+  other.set(std::vector<float>(B * I * O, 1.0f));
+  run(rt, [&] {
+    rt.transpose(x, xt);
+    rt.mult(xt, g, prod);
+    rt.exp(prod, e);
+    rt.mult(xt, g, prod);
+    rt.copy(other, prod); // the second product is dead
+  });
+  {
+    const auto ge = host(e), gp = host(prod);
+    for (size_t b = 0; b < B; ++b)
+      for (size_t i = 0; i < I; ++i)
+        for (size_t o = 0; o < O; ++o) {
+          CHECK_NEAR(ge[(b * I + i) * O + o], std::exp(per(b, i, o)), 1e-4);
+          CHECK(gp[(b * I + i) * O + o] == 1.0f);
+        }
+  }
+  // 3. a partial sum (one of two batch dims) runs the batched product first
+  Tensor x4({2, B, T, I}), g4({2, B, T, O}), xt4({2, B, I, T}), p4({2, B, I, O}), s4({B, I, O});
+  std::vector<float> x4v(xv), g4v(gv);
+  x4v.insert(x4v.end(), xv.begin(), xv.end());
+  g4v.insert(g4v.end(), gv.begin(), gv.end());
+  x4.set(std::span<const float>(x4v));
+  g4.set(std::span<const float>(g4v));
+  run(rt, [&] {
+    rt.transpose(x4, xt4);
+    rt.mult(xt4, g4, p4);
+    rt.sum_to_shape(p4, std::vector<uint32_t>{B, I, O}, s4);
+  });
+  {
+    const auto got = host(s4);
+    for (size_t b = 0; b < B; ++b)
+      for (size_t i = 0; i < I; ++i)
+        for (size_t o = 0; o < O; ++o) CHECK_NEAR(got[(b * I + i) * O + o], 2 * per(b, i, o), 1e-5);
+  }
+}
+
 void sqe(hip::Runtime &rt) {
   Tensor p({2, 3}), t({2, 3}), row({3}), o({2, 3}), ob({2, 3});
   fill(p, {1, -2, 3.5f, 0, 10, -7});
@@ -825,6 +912,7 @@ int main(int argc, char **argv) {
                  [&] { graph_mode_scratch_is_not_reused_within_a_capture(rt); });
     harness::run("sqe", [&] { sqe(rt); });
     harness::run("deferred_views", [&] { deferred_views(rt); });
+    harness::run("deferred_products", [&] { deferred_products(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
