@@ -173,6 +173,36 @@ template <typename T> T *out(RTensor<HIP, T> &t) {
   return p;
 }
 
+// Before an op overwrites every element of `o` without reading it: views
+// and products still pending on o's block keep that block -- it moves to a
+// storage of their own -- and o's storage takes a fresh block from the
+// pool, so nothing is copied. (The executor rewrites its node buffers each
+// step while views of last step's values are still pending.)
+void move_aside(Tensor &o) {
+  auto &views = pending_views();
+  if (views.empty()) return;
+  auto *os = o.get_storage();
+  const void *base = os->data();
+  const auto reads = [base](const PendingView &v) {
+    return v.source.get_storage()->data() == base ||
+           (v.product && v.product->b.get_storage()->data() == base);
+  };
+  if (std::none_of(views.begin(), views.end(), [&](const auto &e) { return reads(e.second); }))
+    return;
+  if (os->size() == 0 || os->size() > UINT32_MAX) return writing(base);
+  // the readers are pointed at the new storage first, then the blocks swap
+  Tensor holder({uint32_t(os->size())});
+  for (auto &[dst, v] : views) {
+    if (v.source.get_storage()->data() == base) v.source = holder;
+    if (v.product && v.product->b.get_storage()->data() == base) {
+      auto plan = std::make_shared<ProductPlan>(*v.product);
+      plan->b = holder;
+      v.product = std::move(plan);
+    }
+  }
+  os->exchange_block(*holder.get_storage());
+}
+
 // Drops the pending view of block `base`, if any, without filling it.
 void drop_view(const void *base) {
   auto &views = pending_views();
@@ -199,9 +229,11 @@ const PendingView *view_of(const Tensor &t) {
 void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
   if (!o.get_storage() || !a.get_storage())
     throw std::logic_error("operation on an uninitialised tensor");
+  if (a.get_storage() == o.get_storage())
+    throw std::invalid_argument("view of a tensor into its own storage");
+  drop_view(o.get_storage()->data());
+  move_aside(o);
   const void *dst = o.get_storage()->data();
-  drop_view(dst);
-  writing(dst);
   shape_type strides(perm.size());
   Tensor source = a;
   if (const PendingView *v = view_of(a)) {
@@ -225,21 +257,26 @@ void defer_reshape(const Tensor &a, Tensor &o) {
     defer_view(a, o, identity);
     return;
   }
-  const void *dst = o.get_storage()->data();
-  drop_view(dst);
-  writing(dst);
+  if (a.get_storage() == o.get_storage())
+    throw std::invalid_argument("view of a tensor into its own storage");
+  drop_view(o.get_storage()->data());
+  move_aside(o);
   in(a);
-  pending_views()[dst] = PendingView{a, o.shape(), o.strides()};
+  pending_views()[o.get_storage()->data()] = PendingView{a, o.shape(), o.strides()};
 }
 
-// The destination of an op that writes every element of `o`: a pending view
-// of o is dropped unfilled (its bytes are dead) unless one of `inputs`
-// shares o's storage and so reads them; views reading o are filled first.
+// The destination of an op that writes every element of `o`: unless one of
+// `inputs` shares o's storage and so reads it, a pending view of o is
+// dropped unfilled (its bytes are dead) and views reading o keep its old
+// block (move_aside); otherwise views reading o are filled first.
 float *dest(Tensor &o, std::initializer_list<const Tensor *> inputs) {
   if (!o.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
   bool read = false;
   for (const Tensor *t : inputs) read = read || t->get_storage() == o.get_storage();
-  if (!read) drop_view(o.get_storage()->data());
+  if (!read) {
+    drop_view(o.get_storage()->data());
+    move_aside(o);
+  }
   return out(o);
 }
 

@@ -17,6 +17,7 @@
 #include <span>
 #include <stdexcept>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 template <typename T> class Storage<hip::HIP, T> {
@@ -75,6 +76,14 @@ public:
       hip::detail::copy(other->data_, data_, size_ * sizeof(T));
     }
     return other;
+  }
+
+  // Exchanges the device blocks of two storages of one size: the runtime
+  // hands a block that pending work still reads to a storage of its own
+  // instead of copying it out before the block is overwritten.
+  void exchange_block(Storage &other) {
+    if (other.size_ != size_) throw std::invalid_argument("exchange_block: sizes differ");
+    std::swap(data_, other.data_);
   }
 
   bool compare(const Storage &other) const {

@@ -722,6 +722,32 @@ void deferred_views(hip::Runtime &rt) {
   expect(sq, {169});
   expect(gslot, {3.0f / 13, 4.0f / 13, 12.0f / 13});
   expect(gsrc, {3, 4, 12});
+  // 7. a source overwritten whole while views of it are pending (the
+  // executor's next step rewriting a node buffer): the views keep the old
+  // values, the source and its aliases see the new ones, and a view of the
+  // new values can be taken again
+  a.set(std::span<const float>(av));
+  Tensor v1({4, 6}), v2({6, 4}), v3({4, 6}), alias({6, 2, 2});
+  run(rt, [&] {
+    rt.transpose(a, v1);
+    rt.copy(a, v2);
+    rt.split_last_dim(a, alias, 2, 2); // alias shares a's storage
+    rt.divide(v2, 0.25f, a);           // a = 4 * old a, read from the pending copy
+    rt.transpose(a, v3);
+  });
+  {
+    const auto h1 = host(v1), h2 = host(v2), h3 = host(v3), ha = host(a), hal = host(alias);
+    for (size_t i = 0; i < 4; ++i)
+      for (size_t j = 0; j < 6; ++j) {
+        CHECK(h1[i * 6 + j] == at(j, i));
+        CHECK(h3[i * 6 + j] == 4.0f * at(j, i));
+      }
+    for (size_t i = 0; i < 24; ++i) {
+      CHECK(h2[i] == av[i]);
+      CHECK(ha[i] == 4.0f * av[i]);
+      CHECK(hal[i] == 4.0f * av[i]);
+    }
+  }
 }
 
 // A per-entry weight gradient as the executor forms it
