@@ -18,6 +18,10 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <memory>
 #include <numeric>
 #include <stdexcept>
 #include <string>
@@ -86,6 +90,119 @@ std::unordered_map<const void *, PendingView> &pending_views() {
   return *views;
 }
 
+// ---- value identities and the result cache ----------------------------------
+// Every block carries the identity of the value it holds: a fresh number
+// whenever a kernel or the host writes it, the source's number when it
+// becomes a copy (a pending copy holds the same bytes), and a number derived
+// from the transpose and its input's number for a transposed view.
+// Filling a pending view changes nothing (the logical contents stay).
+//
+// The reference executor evaluates a gradient expression once per path to
+// a leaf (the local gradients of include/passes/execute.h are recomputed
+// for every use of a node), so its backward computes the same products
+// from the same values several times. An op whose code, parameters, input
+// values and shapes and output shape match a cached result whose block
+// still holds that value makes its destination a pending copy of that block
+// instead of running (`reuse`); results are cached (`remember`) up to a byte
+// budget, least recently used first out. Equal identities mean equal bytes,
+// so results are exactly those of running every op.
+using ValueId = uint64_t;
+ValueId g_next_value = 1;
+ValueId fresh_value() { return g_next_value++; }
+
+std::unordered_map<const void *, ValueId> &block_values() {
+  static auto *values = new std::unordered_map<const void *, ValueId>();
+  return *values;
+}
+ValueId value_of(const void *block) {
+  auto [it, inserted] = block_values().try_emplace(block, 0);
+  if (inserted) it->second = fresh_value();
+  return it->second;
+}
+void set_value(const void *block, ValueId v) { block_values()[block] = v; }
+void written(const void *block) { set_value(block, fresh_value()); }
+
+struct MemoKey {
+  std::vector<uint64_t> words;
+  bool operator==(const MemoKey &o) const { return words == o.words; }
+};
+struct MemoKeyHash {
+  size_t operator()(const MemoKey &k) const {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (uint64_t w : k.words) {
+      h ^= w;
+      h *= 0x100000001b3ull;
+    }
+    return size_t(h);
+  }
+};
+struct MemoEntry {
+  ValueId value;
+  Tensor result; // holds the block
+  size_t bytes;
+  std::list<MemoKey>::iterator age;
+};
+struct ResultCache {
+  std::unordered_map<MemoKey, MemoEntry, MemoKeyHash> entries;
+  std::list<MemoKey> ages;                        // most recent first
+  std::unordered_map<const void *, int> blocks;   // entries per result block
+  std::unordered_map<MemoKey, ValueId, MemoKeyHash> derived; // transposed views
+  size_t bytes = 0;
+};
+ResultCache &cache() {
+  static auto *c = new ResultCache();
+  return *c;
+}
+// Byte budget of the cache; TEMPLIT_HIP_RESULT_CACHE_MB overrides (0 turns
+// reuse off).
+size_t cache_budget() {
+  static const size_t budget = [] {
+    const char *env = std::getenv("TEMPLIT_HIP_RESULT_CACHE_MB");
+    return env ? size_t(std::strtoull(env, nullptr, 10)) << 20 : size_t(1) << 30;
+  }();
+  return budget;
+}
+
+struct KeyBuilder {
+  MemoKey key;
+  explicit KeyBuilder(uint32_t op) { key.words.push_back(op); }
+  template <typename T> KeyBuilder &tensor(const RTensor<HIP, T> &t) {
+    key.words.push_back(t.get_storage() ? value_of(t.get_storage()->data()) : 0);
+    dims(t.shape());
+    return *this;
+  }
+  KeyBuilder &dims(std::span<const uint32_t> d) {
+    key.words.push_back(d.size());
+    key.words.insert(key.words.end(), d.begin(), d.end());
+    return *this;
+  }
+  KeyBuilder &scalar(float v) {
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    key.words.push_back(bits);
+    return *this;
+  }
+};
+
+void forget(std::unordered_map<MemoKey, MemoEntry, MemoKeyHash>::iterator it) {
+  ResultCache &c = cache();
+  c.bytes -= it->second.bytes;
+  c.ages.erase(it->second.age);
+  const void *block = it->second.result.get_storage()->data();
+  if (--c.blocks[block] == 0) c.blocks.erase(block);
+  MemoEntry dead = std::move(it->second); // released after the erase
+  c.entries.erase(it);
+}
+
+// The derived identity of a transposed view of value `v`.
+ValueId derived_value(MemoKey &&key) {
+  auto &derived = cache().derived;
+  if (derived.size() > (size_t(1) << 16)) derived.clear(); // new numbers from here on
+  auto [it, inserted] = derived.try_emplace(std::move(key), 0);
+  if (inserted) it->second = fresh_value();
+  return it->second;
+}
+
 bool contiguous(std::span<const uint32_t> shape, std::span<const uint32_t> strides) {
   uint64_t expect = 1;
   for (size_t i = shape.size(); i-- > 0;) {
@@ -146,9 +263,15 @@ void storage_hook(const void *base, int kind) {
   if (kind == detail::kAccessShutdown) { // the context goes: drop every view
     auto dead = std::move(pending_views());
     pending_views().clear();
+    auto dead_results = std::move(cache().entries);
+    cache().entries.clear();
+    cache().ages.clear();
+    cache().blocks.clear();
+    cache().bytes = 0;
     return;
   }
   if (kind == detail::kAccessRelease) {
+    block_values().erase(base); // the pool may hand the block out again
     auto &views = pending_views();
     const auto it = views.find(base);
     if (it == views.end()) return;
@@ -156,8 +279,12 @@ void storage_hook(const void *base, int kind) {
     views.erase(it);
     return;
   }
-  if (kind == detail::kAccessRead) reading(base);
-  else writing(base);
+  if (kind == detail::kAccessRead) {
+    reading(base);
+  } else {
+    writing(base);
+    written(base);
+  }
 }
 
 template <typename T> const T *in(const RTensor<HIP, T> &t) {
@@ -170,6 +297,7 @@ template <typename T> T *out(RTensor<HIP, T> &t) {
   if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
   T *p = t.get_storage()->data();
   if constexpr (std::is_same_v<T, float>) writing(p);
+  written(p);
   return p;
 }
 
@@ -180,17 +308,20 @@ template <typename T> T *out(RTensor<HIP, T> &t) {
 // step while views of last step's values are still pending.)
 void move_aside(Tensor &o) {
   auto &views = pending_views();
-  if (views.empty()) return;
+  ResultCache &c = cache();
   auto *os = o.get_storage();
   const void *base = os->data();
   const auto reads = [base](const PendingView &v) {
     return v.source.get_storage()->data() == base ||
            (v.product && v.product->b.get_storage()->data() == base);
   };
-  if (std::none_of(views.begin(), views.end(), [&](const auto &e) { return reads(e.second); }))
+  const bool cached = c.blocks.count(base) > 0;
+  if (!cached &&
+      std::none_of(views.begin(), views.end(), [&](const auto &e) { return reads(e.second); }))
     return;
   if (os->size() == 0 || os->size() > UINT32_MAX) return writing(base);
-  // the readers are pointed at the new storage first, then the blocks swap
+  // the readers (and cached results) are pointed at the new storage first,
+  // then the blocks swap; the old block keeps its value identity
   Tensor holder({uint32_t(os->size())});
   for (auto &[dst, v] : views) {
     if (v.source.get_storage()->data() == base) v.source = holder;
@@ -200,7 +331,17 @@ void move_aside(Tensor &o) {
       v.product = std::move(plan);
     }
   }
+  if (cached) {
+    std::vector<MemoKey> stale;
+    for (auto &[key, e] : c.entries) {
+      if (e.result.get_storage()->data() != base) continue;
+      if (e.result.numel() == os->size()) e.result = holder.view(e.result.shape());
+      else stale.push_back(key);
+    }
+    for (const MemoKey &key : stale) forget(c.entries.find(key));
+  }
   os->exchange_block(*holder.get_storage());
+  written(os->data());
 }
 
 // Drops the pending view of block `base`, if any, without filling it.
@@ -246,6 +387,15 @@ void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
   if (source.get_storage() == o.get_storage())
     throw std::invalid_argument("view of a tensor into its own storage");
   pending_views()[dst] = PendingView{std::move(source), o.shape(), std::move(strides)};
+  // a copy holds a's value; a transposed view a value derived from it
+  bool identity = o.shape() == a.shape();
+  for (size_t d = 0; d < perm.size(); ++d) identity = identity && perm[d] == d;
+  if (identity) {
+    set_value(dst, value_of(a.get_storage()->data()));
+  } else {
+    std::vector<uint32_t> order(perm.begin(), perm.end());
+    set_value(dst, derived_value(std::move(KeyBuilder(kTranspose).tensor(a).dims(order).key)));
+  }
 }
 
 // `o` (same element count, another shape) becomes a view of the elements
@@ -263,6 +413,7 @@ void defer_reshape(const Tensor &a, Tensor &o) {
   move_aside(o);
   in(a);
   pending_views()[o.get_storage()->data()] = PendingView{a, o.shape(), o.strides()};
+  set_value(o.get_storage()->data(), value_of(a.get_storage()->data())); // the same bytes
 }
 
 // The destination of an op that writes every element of `o`: unless one of
@@ -278,6 +429,54 @@ float *dest(Tensor &o, std::initializer_list<const Tensor *> inputs) {
     move_aside(o);
   }
   return out(o);
+}
+
+// A cached result for `key`: o already holds it, or o becomes a pending copy
+// of the cached block (its old contents treated as by an op that
+// overwrites it whole). False when there is none and the op must run.
+bool reuse(const MemoKey &key, Tensor &o) {
+  ResultCache &c = cache();
+  if (cache_budget() == 0 || !o.get_storage() || c.entries.empty()) return false;
+  const auto it = c.entries.find(key);
+  if (it == c.entries.end()) return false;
+  MemoEntry &e = it->second;
+  if (value_of(e.result.get_storage()->data()) != e.value || e.result.shape() != o.shape()) {
+    forget(it); // the block was written since
+    return false;
+  }
+  c.ages.splice(c.ages.begin(), c.ages, e.age);
+  if (value_of(o.get_storage()->data()) == e.value) return true;
+  const Tensor source = e.result; // (defer_view may reorder the cache)
+  std::vector<size_t> identity(o.shape().size());
+  std::iota(identity.begin(), identity.end(), size_t(0));
+  defer_view(source, o, identity);
+  return true;
+}
+
+// Caches o (just written by the op `key` describes) as that op's result.
+void remember(MemoKey &&key, const Tensor &o) {
+  ResultCache &c = cache();
+  const size_t budget = cache_budget();
+  if (budget == 0 || !o.get_storage() || o.numel() == 0) return;
+  const size_t bytes = o.numel() * sizeof(float);
+  if (bytes > budget / 4) return;
+  if (const auto it = c.entries.find(key); it != c.entries.end()) forget(it);
+  const void *block = o.get_storage()->data();
+  c.ages.push_front(key);
+  c.entries.emplace(std::move(key), MemoEntry{value_of(block), o, bytes, c.ages.begin()});
+  ++c.blocks[block];
+  c.bytes += bytes;
+  while (c.bytes > budget) forget(c.entries.find(c.ages.back()));
+}
+
+// An op that writes every element of o and whose result `key` determines:
+// a cached result is reused, else `launch(destination pointer)` runs (with
+// dest's treatment of o) and its result is cached.
+template <typename F>
+void cached(KeyBuilder &key, Tensor &o, std::initializer_list<const Tensor *> inputs, F &&launch) {
+  if (reuse(key.key, o)) return;
+  launch(dest(o, inputs));
+  remember(std::move(key.key), o);
 }
 
 // An operand read through its strides: a pending view reads its source
@@ -519,10 +718,14 @@ Runtime::GraphStats Runtime::graph_stats() const { return state_->stats; }
 // ---- elementwise (runtime.cpp:65-136, 321-373, 1073-1081, 1170-1186) -------
 
 namespace {
-void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn, const char *what) {
+void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn, const char *what,
+            uint32_t op) {
   broadcast_strides(a.shape(), a.strides(), o.shape()); // shape checks first
   broadcast_strides(b.shape(), b.strides(), o.shape());
   if (o.numel() == 0) return;
+  KeyBuilder key(op);
+  key.tensor(a).tensor(b).dims(o.shape());
+  if (reuse(key.key, o)) return;
   // An in-place op on a destination that is still a view (a gradient slot
   // holding a copy of its first contribution, then add(slot, g, slot),
   // context.h:73-89): the op writes every element of o, so the inputs that
@@ -543,6 +746,8 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
     check(fn(oa.ptr, ob.ptr, o.get_storage()->data(), uint32_t(o.shape().size()),
              o.shape().data(), sa.data(), sb.data(), stream()),
           what);
+    written(o.get_storage()->data());
+    remember(std::move(key.key), o);
     return;
   }
   // the destination first: views of it are filled before it is written
@@ -553,83 +758,86 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   check(fn(oa.ptr, ob.ptr, dst, uint32_t(o.shape().size()), o.shape().data(), sa.data(),
            sb.data(), stream()),
         what);
+  remember(std::move(key.key), o);
 }
 
-void unary(const Tensor &a, Tensor &o, UnaryFn fn, const char *what) {
+void unary(const Tensor &a, Tensor &o, UnaryFn fn, const char *what, uint32_t op) {
   require_same_count(a, o, what);
   if (o.numel() == 0) return;
-  float *dst = dest(o, {&a});
-  check(fn(in(a), dst, o.numel(), stream()), what);
+  KeyBuilder key(op);
+  key.tensor(a).dims(o.shape());
+  cached(key, o, {&a}, [&](float *dst) { check(fn(in(a), dst, o.numel(), stream()), what); });
 }
 
-void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *what) {
+void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *what, uint32_t op) {
   if (a.shape() != o.shape())
     throw std::invalid_argument("scalar operation input and output shapes must match");
   if (o.numel() == 0) return;
-  float *dst = dest(o, {&a});
-  check(fn(in(a), v, dst, o.numel(), stream()), what);
+  KeyBuilder key(op);
+  key.tensor(a).scalar(v);
+  cached(key, o, {&a}, [&](float *dst) { check(fn(in(a), v, dst, o.numel(), stream()), what); });
 }
 } // namespace
 
 void Runtime::add(const Tensor &a, const Tensor &b, Tensor &o) {
   require_recording("add");
   note(kAdd, o.shape());
-  binary(*this, a, b, o, tlh_add, "add");
+  binary(*this, a, b, o, tlh_add, "add", kAdd);
 }
 void Runtime::sub(const Tensor &a, const Tensor &b, Tensor &o) {
   require_recording("sub");
   note(kSub, o.shape());
-  binary(*this, a, b, o, tlh_sub, "sub");
+  binary(*this, a, b, o, tlh_sub, "sub", kSub);
 }
 void Runtime::hadamard(const Tensor &a, const Tensor &b, Tensor &o) {
   require_recording("hadamard");
   note(kHadamard, o.shape());
-  binary(*this, a, b, o, tlh_hadamard, "hadamard");
+  binary(*this, a, b, o, tlh_hadamard, "hadamard", kHadamard);
 }
 void Runtime::divide(const Tensor &a, const Tensor &b, Tensor &o) {
   require_recording("divide");
   note(kDivide, o.shape());
-  binary(*this, a, b, o, tlh_divide, "divide");
+  binary(*this, a, b, o, tlh_divide, "divide", kDivide);
 }
 void Runtime::add(const Tensor &a, kernel_type v, Tensor &o) {
   require_recording("add");
   note(kAddScalar, o.shape());
-  scalar_op(a, v, o, tlh_add_scalar, "add_scalar");
+  scalar_op(a, v, o, tlh_add_scalar, "add_scalar", kAddScalar);
 }
 void Runtime::divide(const Tensor &a, kernel_type v, Tensor &o) {
   require_recording("divide");
   note(kDivideScalar, o.shape());
-  scalar_op(a, v, o, tlh_divide_scalar, "divide_scalar");
+  scalar_op(a, v, o, tlh_divide_scalar, "divide_scalar", kDivideScalar);
 }
 void Runtime::pow(const Tensor &a, kernel_type v, Tensor &o) {
   require_recording("pow");
   note(kPow, o.shape());
-  scalar_op(a, v, o, tlh_pow_scalar, "pow_scalar");
+  scalar_op(a, v, o, tlh_pow_scalar, "pow_scalar", kPow);
 }
 void Runtime::sigmoid(const Tensor &a, Tensor &o) {
   require_recording("sigmoid");
   note(kSigmoid, o.shape());
-  unary(a, o, tlh_sigmoid, "sigmoid");
+  unary(a, o, tlh_sigmoid, "sigmoid", kSigmoid);
 }
 void Runtime::sqrt(const Tensor &a, Tensor &o) {
   require_recording("sqrt");
   note(kSqrt, o.shape());
-  unary(a, o, tlh_sqrt, "sqrt");
+  unary(a, o, tlh_sqrt, "sqrt", kSqrt);
 }
 void Runtime::exp(const Tensor &a, Tensor &o) {
   require_recording("exp");
   note(kExp, o.shape());
-  unary(a, o, tlh_exp, "exp");
+  unary(a, o, tlh_exp, "exp", kExp);
 }
 void Runtime::GELU(const Tensor &a, Tensor &o) {
   require_recording("GELU");
   note(kGelu, o.shape());
-  unary(a, o, tlh_gelu, "GELU");
+  unary(a, o, tlh_gelu, "GELU", kGelu);
 }
 void Runtime::GELU_derivative(const Tensor &a, Tensor &o) {
   require_recording("GELU_derivative");
   note(kGeluDerivative, o.shape());
-  unary(a, o, tlh_gelu_derivative, "GELU_derivative");
+  unary(a, o, tlh_gelu_derivative, "GELU_derivative", kGeluDerivative);
 }
 
 void Runtime::copy(const Tensor &a, Tensor &o) {
@@ -694,6 +902,9 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
     check(tlh_fill_f32(out(o), 0.0f, o.numel(), stream()), "mult");
     return;
   }
+  KeyBuilder key(kMult);
+  key.tensor(a).tensor(b).dims(o.shape());
+  if (reuse(key.key, o)) return;
   // the destination first (views of it are filled before it is written),
   // then the operands: a pending transpose is read through its strides
   float *dst = dest(o, {&a, &b});
@@ -739,9 +950,11 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
     auto plan = std::make_shared<ProductPlan>(
         ProductPlan{*ob.holder, M, K, N, a_rs, a_cs, b_rs, b_cs, vb.shape, vb.sa, vb.sb, vb.sc});
     pending_views()[dst] = PendingView{*oa.holder, o.shape(), o.strides(), std::move(plan)};
+    remember(std::move(key.key), o);
     return;
   }
   run_product(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, vb, ws_elems);
+  remember(std::move(key.key), o);
 }
 
 // Swap of two dims (runtime.cpp:529-569): a view of `a` filled on demand.
@@ -799,7 +1012,10 @@ void Runtime::sum(const Tensor &a, Tensor &o) { // runtime.cpp:506-518
   require_recording("sum");
   if (o.numel() != 1) throw std::invalid_argument("sum destination must hold one element");
   note(kSum, a.shape());
-  check(tlh_sum(in(a), a.numel(), out(o), stream()), "sum");
+  KeyBuilder key(kSum);
+  key.tensor(a).dims(o.shape());
+  cached(key, o, {&a},
+         [&](float *dst) { check(tlh_sum(in(a), a.numel(), dst, stream()), "sum"); });
 }
 
 void Runtime::sum(const Tensor &a, size_t axis, Tensor &o) { // runtime.cpp:520-527
@@ -837,6 +1053,17 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
     if (a.get_storage() != o.get_storage() && o.numel() > 0) defer_reshape(a, o);
     return;
   }
+  KeyBuilder key(kSumToShape);
+  key.tensor(a).dims(o.shape());
+  if (reuse(key.key, o)) return;
+  reduce_to(a, aligned, o);
+  remember(std::move(key.key), o);
+}
+
+// The reducing part of sum_to_shape (`aligned`: the target right-aligned to
+// a's rank).
+void Runtime::reduce_to(const Tensor &a, const std::vector<uint32_t> &aligned, Tensor &o) {
+  const auto &as = a.shape();
   // The sum over every batch dim of a pending batched product whose entries
   // chain into K: one product over K * entries, written straight into o.
   // `a` stays pending (its sources are unchanged).
@@ -868,16 +1095,16 @@ void Runtime::sum_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
   size_t ws_elems = 0;
   check(tlh_sum_to_shape_workspace(uint32_t(as.size()), as.data(), aligned.data(), &ws_elems),
         "sum_to_shape");
+  float *dst = dest(o, {&a});
   if (ws_elems == 0) {
-    check(tlh_sum_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(),
-                           stream()),
+    check(tlh_sum_to_shape(in(a), dst, uint32_t(as.size()), as.data(), aligned.data(), stream()),
           "sum_to_shape");
     return;
   }
   // Row-chunk partials of a tall column sum, returned to the pool on exit
   // (stream-ordered reuse; held back while a graph is being captured).
   Tensor partials({uint32_t(ws_elems)});
-  check(tlh_sum_to_shape_ws(in(a), out(o), uint32_t(as.size()), as.data(), aligned.data(),
+  check(tlh_sum_to_shape_ws(in(a), dst, uint32_t(as.size()), as.data(), aligned.data(),
                             out(partials), ws_elems, stream()),
         "sum_to_shape");
 }
@@ -924,7 +1151,11 @@ void Runtime::softmax(const Tensor &x, Tensor &o) { // runtime.cpp:747-766
   const Rows r = as_rows(x, "softmax");
   if (o.shape() != x.shape()) throw std::invalid_argument("softmax destination has incorrect shape");
   note(kSoftmax, o.shape());
-  check(tlh_softmax(in(x), out(o), r.rows, r.cols, stream()), "softmax");
+  if (r.rows == 0) return;
+  KeyBuilder key(kSoftmax);
+  key.tensor(x);
+  cached(key, o, {&x},
+         [&](float *dst) { check(tlh_softmax(in(x), dst, r.rows, r.cols, stream()), "softmax"); });
 }
 
 void Runtime::cross_entropy(const Tensor &logits, const IndexTensor &targets, Tensor &o) {
@@ -936,8 +1167,12 @@ void Runtime::cross_entropy(const Tensor &logits, const IndexTensor &targets, Te
   note(kCrossEntropy, logits.shape());
   const Rows r = as_rows(logits, "cross_entropy");
   if (r.rows == 0) return;
-  check(tlh_cross_entropy_rows(in(logits), in(targets), out(o), r.rows, r.cols, stream()),
-        "cross_entropy");
+  KeyBuilder key(kCrossEntropy);
+  key.tensor(logits).tensor(targets).dims(o.shape());
+  cached(key, o, {&logits}, [&](float *dst) {
+    check(tlh_cross_entropy_rows(in(logits), in(targets), dst, r.rows, r.cols, stream()),
+          "cross_entropy");
+  });
 }
 
 void Runtime::cross_entropy_derivative(const Tensor &logits, const IndexTensor &targets,
@@ -949,9 +1184,13 @@ void Runtime::cross_entropy_derivative(const Tensor &logits, const IndexTensor &
   note(kCrossEntropyDerivative, o.shape());
   const Rows r = as_rows(logits, "cross_entropy_derivative");
   if (r.rows == 0) return;
-  check(tlh_cross_entropy_rows_backward(in(logits), in(targets), out(o), r.rows, r.cols, nullptr,
-                                        stream()),
-        "cross_entropy_derivative");
+  KeyBuilder key(kCrossEntropyDerivative);
+  key.tensor(logits).tensor(targets);
+  cached(key, o, {&logits}, [&](float *dst) {
+    check(tlh_cross_entropy_rows_backward(in(logits), in(targets), dst, r.rows, r.cols, nullptr,
+                                          stream()),
+          "cross_entropy_derivative");
+  });
 }
 
 void Runtime::RMS(const Tensor &a, Tensor &o) { // runtime.cpp:1031-1058
@@ -965,9 +1204,13 @@ void Runtime::RMS_impl(const Tensor &a, Tensor &o) {
     throw std::invalid_argument("RMS destination has incorrect shape");
   note(kRms, a.shape());
   if (a.numel() == 0) return;
-  check(tlh_rms(in(a), out(o), a.numel() / a.shape().back(), a.shape().back(), kRmsEpsilon,
-                stream()),
-        "RMS");
+  KeyBuilder key(kRms);
+  key.tensor(a);
+  cached(key, o, {&a}, [&](float *dst) {
+    check(tlh_rms(in(a), dst, a.numel() / a.shape().back(), a.shape().back(), kRmsEpsilon,
+                  stream()),
+          "RMS");
+  });
 }
 
 void Runtime::RMSNorm(const Tensor &a, Tensor &o) { // runtime.cpp:1060-1072
@@ -976,9 +1219,13 @@ void Runtime::RMSNorm(const Tensor &a, Tensor &o) { // runtime.cpp:1060-1072
   if (a.shape().empty()) throw std::invalid_argument("RMSNorm requires rank >= 1");
   note(kRmsNorm, a.shape());
   if (a.numel() == 0) return;
-  check(tlh_rms_norm(in(a), nullptr, out(o), nullptr, a.numel() / a.shape().back(),
-                     a.shape().back(), kRmsEpsilon, stream()),
-        "RMSNorm");
+  KeyBuilder key(kRmsNorm);
+  key.tensor(a);
+  cached(key, o, {&a}, [&](float *dst) {
+    check(tlh_rms_norm(in(a), nullptr, dst, nullptr, a.numel() / a.shape().back(),
+                       a.shape().back(), kRmsEpsilon, stream()),
+          "RMSNorm");
+  });
 }
 
 // ---- embedding (runtime.cpp:920-1030) ------------------------------------------------
@@ -991,9 +1238,13 @@ void Runtime::embedding_lookup(const Tensor &w, const IndexTensor &ids, Tensor &
   if (o.shape() != expected) throw std::invalid_argument("embedding output shape does not match IDs");
   note(kEmbedding, o.shape());
   if (o.numel() == 0) return;
-  check(tlh_embedding_lookup(in(w), w.shape()[0], w.shape()[1], in(ids), ids.numel(), out(o),
-                             stream()),
-        "embedding_lookup");
+  KeyBuilder key(kEmbedding);
+  key.tensor(w).tensor(ids);
+  cached(key, o, {&w}, [&](float *dst) {
+    check(tlh_embedding_lookup(in(w), w.shape()[0], w.shape()[1], in(ids), ids.numel(), dst,
+                               stream()),
+          "embedding_lookup");
+  });
 }
 
 void Runtime::gather_rows(const Tensor &values, const IndexTensor &ids, Tensor &o) {
@@ -1070,6 +1321,7 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
     check(tlh_clip_gradient(copy.source.get_storage()->data(), in(s), max_norm,
                             o.get_storage()->data(), g.numel(), stream()),
           "clip_gradient");
+    written(o.get_storage()->data());
     return;
   }
   float *dst = dest(o, {&g, &s});
@@ -1104,9 +1356,13 @@ void Runtime::RMSNorm(const Tensor &a, const Tensor &gain, kernel_type epsilon, 
     throw std::invalid_argument("RMSNorm gain must have one value per column");
   note(kRmsNormGain, a.shape());
   if (r.rows == 0) return;
-  check(tlh_rms_norm(in(a), has_gain ? in(gain) : nullptr, out(o), nullptr, r.rows, r.cols,
-                     epsilon, stream()),
-        "RMSNorm");
+  KeyBuilder key(kRmsNormGain);
+  key.tensor(a).tensor(gain).scalar(epsilon);
+  cached(key, o, {&a, &gain}, [&](float *dst) {
+    check(tlh_rms_norm(in(a), has_gain ? in(gain) : nullptr, dst, nullptr, r.rows, r.cols,
+                       epsilon, stream()),
+          "RMSNorm");
+  });
 }
 
 void Runtime::softmax_derivative(const Tensor &grad, const Tensor &y, Tensor &o) {
@@ -1116,8 +1372,12 @@ void Runtime::softmax_derivative(const Tensor &grad, const Tensor &y, Tensor &o)
   const Rows r = as_rows(y, "softmax_derivative");
   note(kSoftmaxDerivative, y.shape());
   if (r.rows == 0) return;
-  check(tlh_softmax_backward(in(grad), in(y), out(o), r.rows, r.cols, stream()),
-        "softmax_derivative");
+  KeyBuilder key(kSoftmaxDerivative);
+  key.tensor(grad).tensor(y);
+  cached(key, o, {&grad, &y}, [&](float *dst) {
+    check(tlh_softmax_backward(in(grad), in(y), dst, r.rows, r.cols, stream()),
+          "softmax_derivative");
+  });
 }
 
 void Runtime::GELU_backward(const Tensor &grad, const Tensor &x, Tensor &o) {
@@ -1126,7 +1386,11 @@ void Runtime::GELU_backward(const Tensor &grad, const Tensor &x, Tensor &o) {
     throw std::invalid_argument("GELU_backward shapes must match");
   note(kGeluBackward, x.shape());
   if (x.numel() == 0) return;
-  check(tlh_gelu_backward(in(grad), in(x), out(o), x.numel(), stream()), "GELU_backward");
+  KeyBuilder key(kGeluBackward);
+  key.tensor(grad).tensor(x);
+  cached(key, o, {&grad, &x}, [&](float *dst) {
+    check(tlh_gelu_backward(in(grad), in(x), dst, x.numel(), stream()), "GELU_backward");
+  });
 }
 
 void Runtime::RMSNorm_derivative(const Tensor &grad, const Tensor &x, Tensor &o) {
@@ -1136,9 +1400,13 @@ void Runtime::RMSNorm_derivative(const Tensor &grad, const Tensor &x, Tensor &o)
   const Rows r = as_rows(x, "RMSNorm_derivative");
   note(kRmsNormDerivative, x.shape());
   if (r.rows == 0) return;
-  check(tlh_rms_norm_backward(in(grad), in(x), nullptr, out(o), nullptr, r.rows, r.cols,
-                              kRmsEpsilon, 0.0f, stream()),
-        "RMSNorm_derivative");
+  KeyBuilder key(kRmsNormDerivative);
+  key.tensor(grad).tensor(x);
+  cached(key, o, {&grad, &x}, [&](float *dst) {
+    check(tlh_rms_norm_backward(in(grad), in(x), nullptr, dst, nullptr, r.rows, r.cols,
+                                kRmsEpsilon, 0.0f, stream()),
+          "RMSNorm_derivative");
+  });
 }
 
 namespace {

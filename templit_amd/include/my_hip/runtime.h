@@ -155,6 +155,9 @@ private:
   void require_recording(const char *op) const;
   void note(uint32_t op, std::span<const uint32_t> shape);
   void RMS_impl(const Tensor &a, Tensor &out);
+  // sum_to_shape's reduction, `aligned` being the target right-aligned to
+  // a's rank
+  void reduce_to(const Tensor &a, const std::vector<uint32_t> &aligned, Tensor &out);
 };
 
 } // namespace hip

@@ -14,6 +14,7 @@
 #include "optimiser/AdamW.h"
 #include "templit_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
@@ -750,6 +751,95 @@ void deferred_views(hip::Runtime &rt) {
   }
 }
 
+// The executor evaluates a gradient expression once per path, so the same
+// op runs again on the same values (include/passes/execute.h): the runtime
+// hands back the earlier result. Whatever it reuses, every result must be
+// what running the op gives, also after inputs, cached blocks or
+// destinations change.
+void repeated_results(hip::Runtime &rt) {
+  const std::vector<float> av = random_values(8 * 16, 31), bv = random_values(16 * 4, 32);
+  Tensor a({8, 16}), b({16, 4}), w({8, 4});
+  a.set(std::span<const float>(av));
+  b.set(std::span<const float>(bv));
+  w.set(std::vector<float>(32, 0.0f));
+  auto prod = [&](const std::vector<float> &x, const std::vector<float> &y, size_t i, size_t j) {
+    double e = 0;
+    for (size_t k = 0; k < 16; ++k) e += double(x[i * 16 + k]) * y[k * 4 + j];
+    return e;
+  };
+  auto expect_prod = [&](const Tensor &t, const std::vector<float> &x, const std::vector<float> &y,
+                         double scale, double shift) {
+    const auto got = host(t);
+    for (size_t i = 0; i < 8; ++i)
+      for (size_t j = 0; j < 4; ++j)
+        CHECK_NEAR(got[i * 4 + j], scale * prod(x, y, i, j) + shift, 1e-4);
+  };
+  // 1. the same chain twice into other destinations, a third time into the
+  // first ones, and once with a changed input
+  Tensor p1({8, 4}), p2({8, 4}), e1({8, 4}), e2({8, 4}), q({8, 4});
+  run(rt, [&] {
+    rt.mult(a, b, p1);
+    rt.add(p1, 1.0f, e1);
+    rt.mult(a, b, p2);   // reused: p2 = p1
+    rt.add(p2, 1.0f, e2); // reused through p2's identity
+    rt.mult(a, b, p1);   // p1 already holds it
+    rt.add(p1, 1.0f, e1);
+    rt.divide(p2, 0.5f, q);
+  });
+  expect_prod(p1, av, bv, 1, 0);
+  expect_prod(p2, av, bv, 1, 0);
+  expect_prod(e1, av, bv, 1, 1);
+  expect_prod(e2, av, bv, 1, 1);
+  expect_prod(q, av, bv, 2, 0);
+  // 2. an input changes (kernel write, host write): the op runs again
+  std::vector<float> a2(av);
+  for (auto &x : a2) x *= 3.0f;
+  Tensor p3({8, 4}), p4({8, 4});
+  run(rt, [&] {
+    rt.divide(a, 1.0f / 3.0f, a); // in place: a = 3a
+    rt.mult(a, b, p3);
+  });
+  expect_prod(p3, a2, bv, 1, 0);
+  a.set(std::span<const float>(av));
+  run(rt, [&] { rt.mult(a, b, p4); });
+  expect_prod(p4, av, bv, 1, 0);
+  // 3. the cached block is overwritten in place, then whole: later reuses
+  // of the product it held still see the product
+  Tensor p5({8, 4}), p6({8, 4}), p7({8, 4});
+  run(rt, [&] {
+    rt.mult(a, b, p5);
+    rt.add(p5, p5, p5); // in place: p5 = 2ab, the cached product is gone from it
+    rt.mult(a, b, p6);  // runs again
+    rt.exp(w, p6);      // p6 overwritten whole: the cached product moves aside
+    rt.mult(a, b, p7);  // reused from the moved block
+  });
+  expect_prod(p5, av, bv, 2, 0);
+  expect_prod(p7, av, bv, 1, 0);
+  // 4. a reused result read by a kernel that needs bytes (fills the copy)
+  Tensor s1({8, 1}), s2({8, 1}), r1({8, 4}), r2({8, 4});
+  run(rt, [&] {
+    rt.sum_to_shape(p7, std::vector<uint32_t>{8, 1}, s1);
+    rt.mult(a, b, r1);
+    rt.sum_to_shape(r1, std::vector<uint32_t>{8, 1}, s2); // r1 and p7 hold one value
+    rt.softmax(r1, r2);
+  });
+  {
+    const auto g1 = host(s1), g2 = host(s2), gr = host(r2);
+    for (size_t i = 0; i < 8; ++i) {
+      double e = 0, mx = -1e30, z = 0;
+      for (size_t j = 0; j < 4; ++j) {
+        e += prod(av, bv, i, j);
+        mx = std::max(mx, prod(av, bv, i, j));
+      }
+      CHECK_NEAR(g1[i], e, 1e-4);
+      CHECK(g1[i] == g2[i]);
+      for (size_t j = 0; j < 4; ++j) z += std::exp(prod(av, bv, i, j) - mx);
+      for (size_t j = 0; j < 4; ++j)
+        CHECK_NEAR(gr[i * 4 + j], std::exp(prod(av, bv, i, j) - mx) / z, 1e-5);
+    }
+  }
+}
+
 // A per-entry weight gradient as the executor forms it
 // (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
 // input, a batched product with the output gradient, then sum_to_shape over
@@ -939,6 +1029,7 @@ int main(int argc, char **argv) {
     harness::run("sqe", [&] { sqe(rt); });
     harness::run("deferred_views", [&] { deferred_views(rt); });
     harness::run("deferred_products", [&] { deferred_products(rt); });
+    harness::run("repeated_results", [&] { repeated_results(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
