@@ -287,10 +287,23 @@ void storage_hook(const void *base, int kind) {
   }
 }
 
+// The device pointer a kernel reads t's elements from. A block that is a
+// pending copy (a contiguous view of its source: the same bytes in the same
+// order) is read at its source, which the view holds; any other pending
+// view or product is filled first.
 template <typename T> const T *in(const RTensor<HIP, T> &t) {
   if (!t.get_storage()) throw std::logic_error("operation on an uninitialised tensor");
   const T *p = t.get_storage()->data();
-  if constexpr (std::is_same_v<T, float>) reading(p);
+  if constexpr (std::is_same_v<T, float>) {
+    auto &views = pending_views();
+    if (!views.empty()) {
+      const auto it = views.find(p);
+      if (it != views.end() && !it->second.product &&
+          contiguous(it->second.shape, it->second.strides))
+        return it->second.source.get_storage()->data();
+      reading(p);
+    }
+  }
   return p;
 }
 template <typename T> T *out(RTensor<HIP, T> &t) {
@@ -381,7 +394,7 @@ void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
     source = v->source;
     for (size_t d = 0; d < perm.size(); ++d) strides[d] = v->strides[perm[d]];
   } else {
-    in(a);
+    reading(a.get_storage()->data()); // a view's source is never pending
     for (size_t d = 0; d < perm.size(); ++d) strides[d] = a.strides()[perm[d]];
   }
   if (source.get_storage() == o.get_storage())
@@ -411,9 +424,17 @@ void defer_reshape(const Tensor &a, Tensor &o) {
     throw std::invalid_argument("view of a tensor into its own storage");
   drop_view(o.get_storage()->data());
   move_aside(o);
-  in(a);
-  pending_views()[o.get_storage()->data()] = PendingView{a, o.shape(), o.strides()};
-  set_value(o.get_storage()->data(), value_of(a.get_storage()->data())); // the same bytes
+  // the same bytes: a's source when a is itself a pending copy, else a
+  // (filled first if it is another pending view)
+  Tensor source = a;
+  const auto it = pending_views().find(a.get_storage()->data());
+  if (it != pending_views().end() && !it->second.product &&
+      contiguous(it->second.shape, it->second.strides))
+    source = it->second.source;
+  else
+    reading(a.get_storage()->data());
+  pending_views()[o.get_storage()->data()] = PendingView{std::move(source), o.shape(), o.strides()};
+  set_value(o.get_storage()->data(), value_of(a.get_storage()->data()));
 }
 
 // The destination of an op that writes every element of `o`: unless one of
@@ -917,8 +938,8 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
                         out_batch),
       std::span(o.strides()).first(ro - 2));
   if (vb.shape.size() > 4) { // the views' batch dims do not merge: fill them
-    oa = {in(a), a.strides()};
-    ob = {in(b), b.strides()};
+    oa = {in(a), a.strides(), &a};
+    ob = {in(b), b.strides(), &b};
     vb = batch;
   }
   const uint32_t a_rs = oa.strides[ra - 2], a_cs = oa.strides[ra - 1];
@@ -979,8 +1000,9 @@ void Runtime::transpose(const Tensor &a, Tensor &o, int32_t dim_a, int32_t dim_b
     defer_view(a, o, perm);
     return;
   }
-  check(tlh_transpose(in(a), out(o), uint32_t(o.shape().size()), o.shape().data(),
-                      strides.data(), stream()),
+  float *dst = out(o); // destinations before sources throughout (see `in`)
+  check(tlh_transpose(in(a), dst, uint32_t(o.shape().size()), o.shape().data(), strides.data(),
+                      stream()),
         "transpose");
 }
 
@@ -1131,7 +1153,8 @@ void Runtime::max_to_shape(const Tensor &a, std::span<const uint32_t> shape, Ten
   if (as.size() > 8) throw std::invalid_argument("max_to_shape supports rank <= 8");
   note(kMaxToShape, o.shape());
   if (o.numel() == 0) return;
-  check(tlh_max_to_shape(in(a), out(o), uint32_t(as.size()), as.data(), shape.data(), stream()),
+  float *dst = out(o);
+  check(tlh_max_to_shape(in(a), dst, uint32_t(as.size()), as.data(), shape.data(), stream()),
         "max_to_shape");
 }
 
@@ -1141,7 +1164,8 @@ void Runtime::argmax(const Tensor &a, IndexTensor &o) {
   if (a.numel() == 0) throw std::invalid_argument("argmax requires a non-empty tensor");
   if (o.numel() != 1) throw std::invalid_argument("argmax destination must hold one index");
   note(kArgmax, a.shape());
-  check(tlh_argmax(in(a), a.numel(), out(o), stream()), "argmax");
+  uint32_t *dst = out(o);
+  check(tlh_argmax(in(a), a.numel(), dst, stream()), "argmax");
 }
 
 // ---- row ops -----------------------------------------------------------------------
@@ -1261,8 +1285,9 @@ void validate_scatter(const Tensor &values, const IndexTensor &ids, const Tensor
 }
 void scatter(const Tensor &values, const IndexTensor &ids, Tensor &dst) {
   if (values.numel() == 0) return;
-  check(tlh_scatter_add_rows(in(values), in(ids), ids.numel(), dst.shape()[1], out(dst),
-                             dst.shape()[0], stream()),
+  float *d = out(dst);
+  check(tlh_scatter_add_rows(in(values), in(ids), ids.numel(), dst.shape()[1], d, dst.shape()[0],
+                             stream()),
         "scatter_add_rows");
 }
 } // namespace
@@ -1274,8 +1299,10 @@ void Runtime::scatter_add_rows(const Tensor &base, const IndexTensor &ids, const
     throw std::invalid_argument("scatter base and destination shapes must match");
   validate_scatter(values, ids, o);
   note(kScatterAdd, o.shape());
-  if (o.numel() && in(base) != out(o))
-    check(tlh_copy(in(base), out(o), o.numel(), stream()), "scatter_add_rows");
+  if (o.numel() && base.get_storage() != o.get_storage()) {
+    float *dst = dest(o, {&base});
+    check(tlh_copy(in(base), dst, o.numel(), stream()), "scatter_add_rows");
+  }
   scatter(values, ids, o);
 }
 
@@ -1340,7 +1367,8 @@ void Runtime::adamW(const Tensor &p, const Tensor &g, Tensor &o, Tensor &m1, Ten
   if (step == 0) throw std::invalid_argument("AdamW step must be greater than zero");
   note(kAdamW, p.shape());
   if (p.numel() == 0) return;
-  check(tlh_adamw(in(p), in(g), out(o), out(m1), out(m2), in(beta1), in(beta2), in(decay), in(lr),
+  float *po = out(o), *pm1 = out(m1), *pm2 = out(m2);
+  check(tlh_adamw(in(p), in(g), po, pm1, pm2, in(beta1), in(beta2), in(decay), in(lr),
                   epsilon, step, p.numel(), stream()),
         "adamW");
 }
@@ -1434,8 +1462,9 @@ void Runtime::causal_attention(const Tensor &q, const Tensor &k, const Tensor &v
   require_lse(lse, d);
   note(kAttention, q.shape());
   if (q.numel() == 0) return;
-  check(tlh_attention_forward(in(q), in(k), in(v), out(o), out(lse), d.b, d.h, d.t, d.d, scale, 1,
-                              0, stream()),
+  float *po = out(o), *plse = out(lse);
+  check(tlh_attention_forward(in(q), in(k), in(v), po, plse, d.b, d.h, d.t, d.d, scale, 1, 0,
+                              stream()),
         "causal_attention");
 }
 
@@ -1454,9 +1483,9 @@ void Runtime::causal_attention_backward(const Tensor &q, const Tensor &k, const 
   // Per-row dot(dO, O) workspace, returned to the pool on exit
   // (stream-ordered reuse; held back while a graph is being captured).
   Tensor delta({d.b, d.h, d.t});
-  check(tlh_attention_backward(in(q), in(k), in(v), in(o), in(grad_out), in(lse), out(delta),
-                               out(grad_q), out(grad_k), out(grad_v), d.b, d.h, d.t, d.d, scale, 1,
-                               0, 0, stream()),
+  float *pd = out(delta), *pq = out(grad_q), *pk = out(grad_k), *pv = out(grad_v);
+  check(tlh_attention_backward(in(q), in(k), in(v), in(o), in(grad_out), in(lse), pd, pq, pk, pv,
+                               d.b, d.h, d.t, d.d, scale, 1, 0, 0, stream()),
         "causal_attention_backward");
 }
 

@@ -51,3 +51,30 @@ def test_reference_executor_on_hip_runtime_at_the_benchmark_shapes():
     proc = _run("--bench-shapes")
     assert proc.returncode == 0, proc.stdout
     assert "drop-in parity ok" in proc.stdout
+
+
+THROUGHPUT_BIN = ROOT / "oracle" / "_ref" / "dropin_throughput"
+
+
+@pytest.mark.skipif(not THROUGHPUT_BIN.exists(),
+                    reason="oracle/_ref/dropin_throughput not built (make -C oracle "
+                           "dropin-throughput)")
+@pytest.mark.gpu
+def test_reference_executor_throughput_at_the_benchmark_config():
+    # src/train.cpp's loop body at V 2048, T 192, d 384, 6 heads, 4 blocks,
+    # batch 32 (6144 tokens per step), eager then graph mode: the step time a
+    # user of the reference executor gets on hip::Runtime. Measured 9.1 ms
+    # eager / 12.5 ms graph mode; the bounds catch a lost optimisation (view
+    # deferral, deferred products, result reuse) rather than noise.
+    proc = subprocess.run([str(THROUGHPUT_BIN), "20", "2"], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout)
+    assert proc.returncode == 0, proc.stdout
+    times = {}
+    for line in proc.stdout.splitlines():
+        mode, _, rest = line.partition(":")
+        if "ms/step" in rest:
+            times[mode.strip()] = float(rest.split("ms/step")[0])
+    assert set(times) == {"eager", "graph mode"}, proc.stdout
+    assert times["eager"] < 12.0, times
+    assert times["graph mode"] < 16.0, times
