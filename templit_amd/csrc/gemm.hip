@@ -634,8 +634,15 @@ __device__ inline void tile_epilogue(const GemmParams &p, const BlockCtx &b, con
 // 16-byte groups) the 32 lanes of each read pass -- rows 0..15 of groups g
 // and g+1, one 16-byte group apart -- hit distinct banks of gfx950's LDS
 // (measured: no bank conflicts; with a stride of BK + 4, or consecutive k
-// blocks per lane group, 13% of the read cycles conflict). Same staging, K loop and epilogues as gemm_mfma_kernel; no
-// bias gradient (the planner keeps those on gemm_mfma_kernel).
+// blocks per lane group, 13% of the read cycles conflict).
+// Row-contiguous operand tiles (A transposed, B not: [BK][rows + pad]) are
+// read with the subtiles interleaved when a wave has 2 or 4 of them in that
+// dimension: row slot r16 of subtile i is row TM*r16 + i of the wave's WM
+// rows (columns alike), so a lane's TM values of one k sit side by side in
+// LDS and come in one ds_read_b64 / b128 instead of TM ds_read_b32; the
+// accumulators are put back in order when they are staged for the
+// epilogue. Same staging, K loop and epilogues as gemm_mfma_kernel,
+// including the bias gradient of the first tile row.
 // LDS floats of gemm_tile16: two stages of both operand tiles.
 template <int BM, int BN, int BK, bool TA, bool TB>
 constexpr int tile16_smem() {
@@ -685,8 +692,11 @@ __device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int a_row0 = wm * WM + r16; // + i*16
-  const int b_col0 = wn * WN + r16; // + j*16
+  // interleaved subtiles of the row-contiguous operand tiles
+  constexpr bool IA = TA && (TM == 2 || TM == 4);
+  constexpr bool IB = !TB && (TN == 2 || TN == 4);
+  const int a_row0 = wm * WM + (IA ? TM * r16 : r16); // + i (interleaved) or i*16
+  const int b_col0 = wn * WN + (IB ? TN * r16 : r16); // + j or j*16
 
   auto compute_tile = [&](int buf) {
     const float *as = smem + buf * (A_TILE + B_TILE);
@@ -696,24 +706,56 @@ __device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int
 #pragma unroll
     for (int s4 = 0; s4 < Q; ++s4) {
       const int kb = 4 * (g + 4 * s4); // first of 4 consecutive k
+      if constexpr (IA) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int m = a_row0 + i * 16;
-        if (!TA) {
-          af[i][s4] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
-        } else {
+        for (int q = 0; q < 4; ++q) {
+          const float *src = as + (kb + q) * A_LD + a_row0;
+          if constexpr (TM == 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(src);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) af[i][s4][q] = as[(kb + q) * A_LD + m];
+            for (int i = 0; i < 4; ++i) af[i][s4][q] = v[i];
+          } else {
+            const float2 v = *reinterpret_cast<const float2 *>(src);
+            af[0][s4][q] = v.x;
+            af[1][s4][q] = v.y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int m = a_row0 + i * 16;
+          if (!TA) {
+            af[i][s4] = *reinterpret_cast<const f4 *>(as + m * A_LD + kb);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) af[i][s4][q] = as[(kb + q) * A_LD + m];
+          }
         }
       }
+      if constexpr (IB) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = b_col0 + j * 16;
-        if (TB) {
-          bf[j][s4] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
-        } else {
+        for (int q = 0; q < 4; ++q) {
+          const float *src = bs + (kb + q) * B_LD + b_col0;
+          if constexpr (TN == 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(src);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) bf[j][s4][q] = bs[(kb + q) * B_LD + n];
+            for (int j = 0; j < 4; ++j) bf[j][s4][q] = v[j];
+          } else {
+            const float2 v = *reinterpret_cast<const float2 *>(src);
+            bf[0][s4][q] = v.x;
+            bf[1][s4][q] = v.y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = b_col0 + j * 16;
+          if (TB) {
+            bf[j][s4] = *reinterpret_cast<const f4 *>(bs + n * B_LD + kb);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bf[j][s4][q] = bs[(kb + q) * B_LD + n];
+          }
         }
       }
     }
@@ -730,6 +772,15 @@ __device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int
     if constexpr (!TA) __builtin_amdgcn_iglp_opt(1);
   };
 
+  // Bias gradient: the blocks of the first tile row also sum the op(B)
+  // tiles they stage (threads = BN columns x 256/BN k groups).
+  // (tiles of 64 and 128 columns; the planner keeps bias gradients off 96)
+  constexpr bool BIAS = 256 % BN == 0;
+  const bool do_bias = BIAS && p.bias_grad != nullptr && ctx.tm == 0;
+  constexpr int BGROUPS = 256 / BN;
+  const int bcol = tid % BN, bgrp = tid / BN;
+  float bsum = 0.f;
+
   const int nk = (k_end > k_begin) ? (k_end - k_begin + BK - 1) / BK : 0;
   if (nk > 0) {
     load_tile(k_begin);
@@ -739,13 +790,28 @@ __device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int
       const int cur = kt & 1;
       if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * BK);
       compute_tile(cur);
+      if constexpr (BIAS) {
+        if (do_bias) {
+          const float *bs = smem + cur * (A_TILE + B_TILE) + A_TILE;
+#pragma unroll
+          for (int kk = bgrp; kk < BK; kk += BGROUPS)
+            bsum += TB ? bs[bcol * B_LD + kk] : bs[kk * B_LD + bcol];
+        }
+      }
       if (kt + 1 < nk) store_tile(cur ^ 1);
       __syncthreads();
     }
   }
+  if constexpr (BIAS) {
+    if (do_bias) {
+      bias_grad_store<BN>(p, ctx, smem, bsum, FULL);
+      __syncthreads(); // smem is the output tile next
+    }
+  }
   // Accumulators -> LDS (free again: the K loop ended with a barrier), then
-  // the row-major epilogue. Lane l holds rows 4*(l/16) + v, column l%16 of
-  // each 16x16 subtile.
+  // the row-major epilogue. Lane l holds row slots 4*(l/16) + v, column slot
+  // l%16 of each 16x16 subtile (interleaved subtiles: slot s of subtile i is
+  // row TM*s + i).
   constexpr int C_LD = BN + 4;
   static_assert(BM * C_LD <= 2 * (A_TILE + B_TILE), "output tile fits the operand buffers");
   float *ct = smem;
@@ -754,8 +820,11 @@ __device__ inline void gemm_tile16(const GemmParams &p, float *smem, int bx, int
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        ct[(wm * WM + i * 16 + 4 * g + v) * C_LD + wn * WN + j * 16 + r16] = acc[i][j][v];
+      for (int v = 0; v < 4; ++v) {
+        const int row = wm * WM + (IA ? TM * (4 * g + v) + i : i * 16 + 4 * g + v);
+        const int col = wn * WN + (IB ? TN * r16 + j : j * 16 + r16);
+        ct[row * C_LD + col] = acc[i][j][v];
+      }
   __syncthreads();
   tile_epilogue<BM, BN, FULL>(p, ctx, ct);
 }
@@ -1106,6 +1175,7 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce(GemmParams p) {
 
 struct Plan {
   int bm, bn, splits, bk = 16;
+  bool m16 = false; // the 16x16x4 MFMA kernel (gemm_tile16) at bm x bn
 };
 
 template <int BM, int BN, int WM, int WN, int BK>
@@ -1186,6 +1256,7 @@ constexpr int kTargetBlocks = 256; // one block per CU at least
 // Process-wide plan override for tuning sweeps (tlh_gemm_set_plan); 0 = the
 // planner decides.
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
+int g_tile16_wgrad = 1; // split weight gradients on the 16x16x4 kernel
 int g_xcd_remap = 1;
 int g_xcd_rects = 1;
 int g_gemv = 1;
@@ -1266,6 +1337,8 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   const bool one_dim = d.sum_batches || d.batch_ndim <= 1;
   if (g_force_bm > 0) {
     const bool can_split = allow_split && one_dim;
+    if (g_force_bm == 16) // 16x16 MFMA, square tiles of g_force_bn, K tile 32
+      return {g_force_bn, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, 32, true};
     if (g_force_bm == 96) { // 16x16 MFMA tiles, no bias gradient
       if (d.bias_grad) return {64, 64, 1, 32};
       // 8 waves over K tiles of 64: no split-K, summed entries of 64 | K
@@ -1305,14 +1378,17 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
   // weight gradients (transposed A, K = tokens) split K below 3 tiles per CU:
   // one long whole-K block per CU runs [1024,1024] x K 8192 at 72 TFLOP/s, 8
-  // splits at 105
+  // splits at 105. With both operand tiles row-contiguous (A transposed, B
+  // not) the 16x16x4 kernel reads them with interleaved subtiles: [384,384]
+  // 38.7 -> 35.9 us, [1536,384] 99.7 -> 84.7, [384,1536] 100.7 -> 86.5,
+  // [384,2048] 104.8 -> 98.1 (K = 6144).
   const size_t split_below = (d.trans_a ? 3 : 1) * size_t(kTargetBlocks);
   if (allow_split && one_dim && tiles < split_below && K >= 2 * kMinSplitK) {
     int splits = 1;
     while (splits < 16 && tiles * size_t(splits) < 3 * size_t(kTargetBlocks) &&
            K / (splits * 2) >= kMinSplitK)
       splits *= 2;
-    if (splits >= 2) return {64, 64, splits, 32};
+    if (splits >= 2) return {64, 64, splits, 32, g_tile16_wgrad && d.trans_a && !d.trans_b};
   }
   return {64, 64, 1, K <= 256 ? 16 : 32};
 }
@@ -1378,7 +1454,7 @@ struct TailSplit {
 
 TailSplit tail_split(const GemmDesc &d, const Plan &plan, int K) {
   TailSplit t;
-  if (!g_tail_split || plan.splits > 1 || plan.bm == 96 || d.bias_grad ||
+  if (!g_tail_split || plan.splits > 1 || plan.bm == 96 || plan.m16 || d.bias_grad ||
       (d.batch > 1 && !d.sum_batches))
     return t;
   // the reduction launch costs a few microseconds: only long K ranges gain
@@ -1550,7 +1626,11 @@ int gemm_main(const Prepared &L, hipStream_t s) {
   const Plan &plan = L.plan;
   const bool ta = L.ta, tb = L.tb, vec = L.vec, full = L.full;
   const dim3 grid = L.grid;
-  if (plan.bm == 96 && plan.bk == 64) {
+  if (plan.m16 && plan.bm == 64) {
+    launch16<64, 64, 32>(p, ta, tb, vec, full, grid, s);
+  } else if (plan.m16 && plan.bm == 128) {
+    launch16<128, 128, 32>(p, ta, tb, vec, full, grid, s);
+  } else if (plan.bm == 96 && plan.bk == 64) {
     launch16x8<96, 96>(p, ta, tb, vec, full, grid, s);
   } else if (plan.bm == 96) {
     launch16<96, 96, 32>(p, ta, tb, vec, full, grid, s);
@@ -1656,7 +1736,9 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   // the tail split off (-3) or on (-4), the XCD rectangles off (-5) or on
   // (-6), the one-row GEMV off (-7) or on (-8), the float4 split-K reduction
   // off (-9) or on (-10), the planner's 96x96 tiles off (-11) or on (-12),
-  // the split-major XCD order off (-13) or on (-14).
+  // the split-major XCD order off (-13) or on (-14), split weight gradients
+  // on the 16x16x4 kernel off (-15) or on (-16). bm = 16 forces the 16x16x4
+  // kernel with square tiles of bn (64 or 128) and a K tile of 32.
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
     return 0;
@@ -1685,7 +1767,12 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
     tlh::g_xcd_zmajor = bk == -14;
     return 0;
   }
+  if (bk == -15 || bk == -16) {
+    tlh::g_tile16_wgrad = bk == -16;
+    return 0;
+  }
   const bool ok = (bm == 0 && bn == 0) || (bm == 96 && bn == 96 && (bk == 32 || bk == 64)) ||
+                  (bm == 16 && (bn == 64 || bn == 128) && bk == 32) ||
                   ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
   if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32 && (bk != 64 || bm != 96)))
     return int(hipErrorInvalidValue);

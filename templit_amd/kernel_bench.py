@@ -126,6 +126,7 @@ def run_gemm(b: Bench, iters: int, sweep: bool, only: str | None = None) -> None
         plans += [(bm, bn, s, bk) for bk in (16, 32) for bm in (64, 128) for bn in (64, 128)
                   for s in (1, 4, 8, 16)]
         plans += [(96, 96, s, 32) for s in (1, 4, 8, 16)] + [(96, 96, 1, 64)]
+        plans += [(16, t, s, 32) for t in (64, 128) for s in (1, 2, 4, 8, 16)]
     for name, M, N, K, ta, tb, bgrad in GEMM_SHAPES:
         if only and only not in name:
             continue

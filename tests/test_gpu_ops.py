@@ -341,6 +341,7 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -10), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -12), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -14), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -16), "set_plan")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
@@ -420,12 +421,10 @@ def test_gemm_split_major_xcd_order(g, forced_plan, M, N, batch):
         assert_close(bg, O.sum_to_shape(dys[j], [N]), rtol=1e-4, atol=1e-3, what=f"db[{j}]")
 
 
-@pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
-@pytest.mark.parametrize("bk", [16, 32])
-def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
-    # Every tile / K-tile plan on a tile-aligned shape (the bounds-free
-    # path), every operand layout, and the weight-gradient form with its
-    # bias gradient, unsplit and split over K.
+def _every_layout(g, forced_plan, bm, bn, bk):
+    # A tile plan on a tile-aligned shape (the bounds-free path), every
+    # operand layout, and the weight-gradient form with its bias gradient,
+    # unsplit and split over K; then ragged edges (the bounds-checked path).
     M, N, K = 256, 384, 512
     for ta in (False, True):
         for tb in (False, True):
@@ -441,10 +440,29 @@ def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
         dw, db = gemm(g, x, dy, ta=True, bias_grad_init=np.zeros(N, np.float32))
         assert_rel(dw.reshape(M, N), O.matmul(x.T, dy), 1e-3, f"dW splits={splits}")
         assert_close(db, O.sum_to_shape(dy, [N]), rtol=1e-4, atol=1e-3, what="db")
-    forced_plan(bm, bn, 1, bk)  # ragged edges (the bounds-checked path)
-    a, b = O.normal((200, 100), 154, 0, 0.5), O.normal((100, 300), 155, 0, 0.5)
-    out, _ = gemm(g, a, b)
-    assert_rel(out.reshape(200, 300), O.matmul(a, b), 1e-3, "ragged")
+    forced_plan(bm, bn, 1, bk)
+    for ta in (False, True):
+        for tb in (False, True):
+            a = O.normal((100, 200) if ta else (200, 100), 154, 0, 0.5)
+            b = O.normal((300, 100) if tb else (100, 300), 155, 0, 0.5)
+            out, _ = gemm(g, a, b, ta, tb)
+            expect = O.matmul(a.T if ta else a, b.T if tb else b)
+            assert_rel(out.reshape(200, 300), expect, 1e-3, f"ragged ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("bm,bn", [(64, 64), (64, 128), (128, 64), (128, 128)])
+@pytest.mark.parametrize("bk", [16, 32])
+def test_gemm_every_tile_plan(g, forced_plan, bm, bn, bk):
+    _every_layout(g, forced_plan, bm, bn, bk)
+
+
+@pytest.mark.parametrize("tile", [64, 128])
+def test_gemm_tile16_square_plans(g, forced_plan, tile):
+    # The 16x16x4 MFMA kernel at 64x64 and 128x128 tiles (set_plan bm = 16):
+    # its row-contiguous operand tiles (A transposed, B not) are read with
+    # interleaved subtiles (b64 / b128 LDS reads), and it carries the bias
+    # gradient of the weight-gradient form.
+    _every_layout(g, forced_plan, 16, tile, 32)
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
