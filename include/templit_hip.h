@@ -323,8 +323,10 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * -12 the planner's 96x96 tiles off / on (default on), bk = -13 / -14 the
  * split-major XCD order of split-K and batched grids off / on (default on;
  * same bits), bk = -15 / -16 split weight gradients (A transposed, B not)
- * on the 16x16x4 kernel off / on (default on); these leave the plan
- * alone. */
+ * on the 16x16x4 kernel off / on (default on), bk = -17 / -18 products with
+ * neither operand transposed on the 16x16x4 kernel where the planner takes
+ * 128x128 / 64x128 tiles, or 64x64 tiles at K >= 384, off / on (default
+ * on); these leave the plan alone. */
 int tlh_gemm_set_plan(int bm, int bn, int splits, int bk);
 
 /* ---------------------------------------------------------------------------

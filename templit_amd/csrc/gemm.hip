@@ -1252,11 +1252,13 @@ inline size_t tiles_for(const GemmDesc &d, int bm, int bn) {
 }
 
 constexpr int kTargetBlocks = 256; // one block per CU at least
+constexpr int kMinTailSplitK = 1024; // shortest K the tail split (below) is used for
 
 // Process-wide plan override for tuning sweeps (tlh_gemm_set_plan); 0 = the
 // planner decides.
 int g_force_bm = 0, g_force_bn = 0, g_force_splits = 0, g_force_bk = 16;
 int g_tile16_wgrad = 1; // split weight gradients on the 16x16x4 kernel
+int g_tile16_rowb = 1;  // products with B row-contiguous on the 16x16x4 kernel
 int g_xcd_remap = 1;
 int g_xcd_rects = 1;
 int g_gemv = 1;
@@ -1369,12 +1371,21 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
     return double(d.M) * double(d.N) /
            (double((d.M + bm - 1) / bm * bm) * double((d.N + bn - 1) / bn * bn));
   };
+  // B row-contiguous in LDS (not transposed, A not transposed either): the
+  // 16x16x4 kernel's interleaved B reads win at 128x128 where those tiles
+  // are taken ([8192,1024].[1024,4096] 559 -> 541 us, [8192,1024].[1024,1024]
+  // 152 -> 137 us, [6144,384].[384,2048] 96 -> 91 us) and at 64x64 for K >=
+  // 384 and below the tail split's K ([768,384].[384,1536] 21.5 -> 19.0
+  // us).
+  const bool row_b = g_tile16_rowb && !d.trans_a && !d.trans_b && K % 32 == 0;
   if (K >= 384 && tiles_for(d, 128, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
-      coverage(128, 128) >= 0.9 * coverage(64, 64))
+      coverage(128, 128) >= 0.9 * coverage(64, 64)) {
+    if (row_b) return {128, 128, 1, 32, true};
     return (K >= 1024 && d.trans_b) ? Plan{64, 128, 1, 16} : Plan{128, 128, 1, 16};
+  }
   if (K >= 1024 && tiles_for(d, 64, 128) * outputs >= 3 * size_t(kTargetBlocks) &&
       coverage(64, 128) >= 0.9 * coverage(64, 64))
-    return {64, 128, 1, 16};
+    return row_b ? Plan{128, 128, 1, 32, true} : Plan{64, 128, 1, 16};
   const size_t tiles = tiles_for(d, 64, 64) * outputs;
   // weight gradients (transposed A, K = tokens) split K below 3 tiles per CU:
   // one long whole-K block per CU runs [1024,1024] x K 8192 at 72 TFLOP/s, 8
@@ -1390,6 +1401,8 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
       splits *= 2;
     if (splits >= 2) return {64, 64, splits, 32, g_tile16_wgrad && d.trans_a && !d.trans_b};
   }
+  // (from K = 1024 the tail split on the 32x32 kernel is taken instead)
+  if (row_b && K >= 384 && K < kMinTailSplitK) return {64, 64, 1, 32, true};
   return {64, 64, 1, K <= 256 ? 16 : 32};
 }
 
@@ -1445,7 +1458,6 @@ int cu_count() {
 // blocks; each remaining tile is cut into `splits` K chunks (multiples of
 // kBK, so no K tile straddles a chunk or a K segment) that spread over the
 // CUs, and gemm_tail_reduce sums them.
-constexpr int kMinTailSplitK = 1024;
 
 struct TailSplit {
   int dp_tiles = 0, tails = 0, splits = 0, k_chunk = 0;
@@ -1737,7 +1749,8 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   // (-6), the one-row GEMV off (-7) or on (-8), the float4 split-K reduction
   // off (-9) or on (-10), the planner's 96x96 tiles off (-11) or on (-12),
   // the split-major XCD order off (-13) or on (-14), split weight gradients
-  // on the 16x16x4 kernel off (-15) or on (-16). bm = 16 forces the 16x16x4
+  // on the 16x16x4 kernel off (-15) or on (-16), products with B not
+  // transposed on the 16x16x4 kernel off (-17) or on (-18). bm = 16 forces the 16x16x4
   // kernel with square tiles of bn (64 or 128) and a K tile of 32.
   if (bk == -1 || bk == -2) {
     tlh::g_xcd_remap = bk == -2;
@@ -1769,6 +1782,10 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
   }
   if (bk == -15 || bk == -16) {
     tlh::g_tile16_wgrad = bk == -16;
+    return 0;
+  }
+  if (bk == -17 || bk == -18) {
+    tlh::g_tile16_rowb = bk == -18;
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || (bm == 96 && bn == 96 && (bk == 32 || bk == 64)) ||

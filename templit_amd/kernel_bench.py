@@ -31,6 +31,10 @@ GEMM_SHAPES = [  # name, M, N, K, trans_a, trans_b, bias gradient
     ("wgrad dd", D, D, R, 1, 0, 1), ("wgrad fd", F, D, R, 1, 0, 1),
     ("wgrad df", D, F, R, 1, 0, 1), ("wgrad dv", D, V, R, 1, 0, 1),
     ("d1024 up", 8192, 4096, 1024, 0, 0, 0), ("d1024 sq", 8192, 1024, 1024, 0, 0, 0),
+    ("c1 matmul", 768, 1536, 384, 0, 0, 0),
+    # the reference executor's forward products read W [in, out] as stored
+    ("nn qkv/o fwd", R, D, D, 0, 0, 0), ("nn w1 fwd", R, F, D, 0, 0, 0),
+    ("nn w2 fwd", R, D, F, 0, 0, 0), ("nn vocab fwd", R, V, D, 0, 0, 0),
 ]
 BUF = 8192 * 4096  # largest operand of the shapes above
 ATTENTION_SHAPES = [(32, 6, 192), (8, 16, 1024)]  # (B, H, T), head dim 64
@@ -141,7 +145,7 @@ def run_gemm(b: Bench, iters: int, sweep: bool, only: str | None = None) -> None
         results = []
         b.mark(f"gemm {name} M{M} N{N} K{K} ta{ta} tb{tb}")
         for plan in plans:
-            if plan[2] > 1 and not bgrad:
+            if plan[2] > 1 and not bgrad and not name.startswith("c1"):
                 continue
             check(b.hip.tlh_gemm_set_plan(*plan), "plan")
             need = ctypes.c_size_t()

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from templit_amd.native import GptProgram, NativeError
+from templit_amd.native import GptProgram, NativeError, check, load_hip
 
 pytestmark = pytest.mark.gpu
 
@@ -203,7 +203,19 @@ def test_stream_choice_follows_the_tile_count():
         prog.close()
 
 
-def test_forward_copies_change_no_bit():
+@pytest.fixture
+def row_b_on_32x32():
+    # The planner runs products with a non-transposed B on the 16x16x4
+    # kernel (a different summation order than the 32x32 kernel the
+    # transposed-B forward uses); for the bitwise comparisons both forms run
+    # on the 32x32 kernel, as they did before that rule.
+    hip = load_hip()
+    check(hip.tlh_gemm_set_plan(0, 0, 0, -17), "set_plan")
+    yield
+    check(hip.tlh_gemm_set_plan(0, 0, 0, -18), "set_plan")
+
+
+def test_forward_copies_change_no_bit(row_b_on_32x32):
     # forward products on K-contiguous weight copies (rebuilt at every
     # forward) against the [in, out] weights: the same products in the same
     # order, so losses, gradients and updated parameters agree bitwise;
@@ -232,7 +244,7 @@ def test_forward_copies_change_no_bit():
         prog.close()
 
 
-def test_forward_copies_change_no_bit_at_the_benchmark_shapes():
+def test_forward_copies_change_no_bit_at_the_benchmark_shapes(row_b_on_32x32):
     # batch 32 x T 192 x d 384 with the 2048-entry vocabulary: the vocab
     # projection [6144, 2048] x K 384 takes 128x128 tiles, transposed-B on
     # the copies; one block keeps the oracle-free check cheap
@@ -250,6 +262,31 @@ def test_forward_copies_change_no_bit_at_the_benchmark_shapes():
             runs.append((prog.losses(), prog.get_grads(), prog.get_params()))
         for got, want, what in zip(runs[0], runs[1], ("losses", "grads", "params")):
             assert np.array_equal(got, want), what
+    finally:
+        prog.close()
+
+
+def test_forward_without_copies_on_the_16x16_kernel():
+    # the default plans: without copies the forward's [in, out] products run
+    # on the 16x16x4 kernel; the steps agree with the copies' to rounding
+    prog = GptProgram(256, 192, 384, 6, 2, 4)
+    try:
+        runs = []
+        for mode in (0, 1):
+            prog.set_forward_copies(mode)
+            prog.init_params(seed=5, std=0.02)
+            prog.set_optimizer(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+            prog.random_batch(seed=6)
+            for _ in range(2):
+                prog.train_step(1.0 / (4 * 192), 1.0)
+            prog.synchronize()
+            runs.append((prog.losses(), prog.get_grads(), prog.get_params()))
+        np.testing.assert_allclose(runs[0][0], runs[1][0], rtol=1e-5, atol=1e-6)
+        g0, g1 = runs[0][1].astype(np.float64), runs[1][1].astype(np.float64)
+        assert np.linalg.norm(g0 - g1) <= 1e-4 * np.linalg.norm(g1)
+        # AdamW's normalised step turns rounding in a near-zero gradient into
+        # up to lr per step and element
+        np.testing.assert_allclose(runs[0][2], runs[1][2], rtol=1e-4, atol=2 * 3e-4)
     finally:
         prog.close()
 

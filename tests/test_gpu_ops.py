@@ -342,6 +342,7 @@ def forced_plan(g):
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -12), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -14), "set_plan")
     check(g.lib.tlh_gemm_set_plan(0, 0, 0, -16), "set_plan")
+    check(g.lib.tlh_gemm_set_plan(0, 0, 0, -18), "set_plan")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (4096, 1024), (1024, 4096), (384, 2048), (100, 68),
