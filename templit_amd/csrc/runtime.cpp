@@ -239,8 +239,27 @@ void materialise(const void *base) {
           "materialise transpose");
 }
 
+// ---- squared norms collected per scalar -------------------------------------
+// Compiled::step(max_norm) accumulates every gradient's squared norm into one
+// scalar, a call per tensor (include/passes/compile.h:241-245), and reads it
+// only in the clips that follow. The calls are collected per scalar and run
+// as one multi-tensor launch plus one add into the scalar when the scalar is
+// read or written, when one of the collected gradients is about to be
+// written, or at submit().
+struct PendingNorm {
+  Tensor s;
+  std::vector<Tensor> grads;
+};
+std::unordered_map<const void *, PendingNorm> &pending_norms() {
+  static auto *norms = new std::unordered_map<const void *, PendingNorm>();
+  return *norms;
+}
+void flush_norm(const void *s_block);           // the collection into this scalar, if any
+void flush_norms_reading(const void *block);    // every collection holding this gradient
+
 // Before a kernel or the host reads block `base`.
 void reading(const void *base) {
+  if (!pending_norms().empty()) flush_norm(base);
   if (!pending_views().empty()) materialise(base);
 }
 
@@ -248,6 +267,10 @@ void reading(const void *base) {
 // first (partial and in-place writes keep the rest), then every view whose
 // source is this block, which needs its current contents.
 void writing(const void *base) {
+  if (!pending_norms().empty()) {
+    flush_norm(base);
+    flush_norms_reading(base);
+  }
   auto &views = pending_views();
   if (views.empty()) return;
   materialise(base);
@@ -263,6 +286,8 @@ void storage_hook(const void *base, int kind) {
   if (kind == detail::kAccessShutdown) { // the context goes: drop every view
     auto dead = std::move(pending_views());
     pending_views().clear();
+    auto dead_norms = std::move(pending_norms());
+    pending_norms().clear();
     auto dead_results = std::move(cache().entries);
     cache().entries.clear();
     cache().ages.clear();
@@ -272,6 +297,10 @@ void storage_hook(const void *base, int kind) {
   }
   if (kind == detail::kAccessRelease) {
     block_values().erase(base); // the pool may hand the block out again
+    if (const auto it = pending_norms().find(base); it != pending_norms().end()) {
+      PendingNorm dead = std::move(it->second); // nobody can read this scalar any more
+      pending_norms().erase(it);
+    }
     auto &views = pending_views();
     const auto it = views.find(base);
     if (it == views.end()) return;
@@ -314,12 +343,54 @@ template <typename T> T *out(RTensor<HIP, T> &t) {
   return p;
 }
 
+void flush_norm(const void *s_block) {
+  auto node = pending_norms().extract(s_block);
+  if (node.empty()) return;
+  PendingNorm pn = std::move(node.mapped());
+  const size_t n = pn.grads.size();
+  // device tables: n gradient pointers, then n element counts (u64 each)
+  std::vector<uint64_t> table(2 * n);
+  for (size_t i = 0; i < n; ++i) {
+    table[i] = reinterpret_cast<uintptr_t>(in(pn.grads[i]));
+    table[n + i] = pn.grads[i].numel();
+  }
+  Tensor tables({uint32_t(4 * n)});
+  tables.get_storage()->write(
+      std::span<const float>(reinterpret_cast<const float *>(table.data()), 4 * n), 0);
+  Tensor partials({uint32_t(TLH_NORM_PARTIALS + 1)}); // the last element takes the sum
+  float *part = out(partials);
+  const float *tab = in(tables);
+  check(tlh_gradient_squared_norm_multi(reinterpret_cast<const float *const *>(tab),
+                                        reinterpret_cast<const uint64_t *>(tab + 2 * n),
+                                        uint32_t(n), part, part + TLH_NORM_PARTIALS, stream()),
+        "accumulate_gradient_squared_norm");
+  float *acc = pn.s.get_storage()->data(); // (not pending: filled when the collection began)
+  const uint32_t one = 1;
+  check(tlh_add(acc, part + TLH_NORM_PARTIALS, acc, 1, &one, &one, &one, stream()),
+        "accumulate_gradient_squared_norm");
+}
+
+void flush_norms_reading(const void *block) {
+  std::vector<const void *> hits;
+  for (const auto &[sb, pn] : pending_norms())
+    for (const Tensor &g : pn.grads)
+      if (g.get_storage()->data() == block) {
+        hits.push_back(sb);
+        break;
+      }
+  for (const void *sb : hits) flush_norm(sb);
+}
+
 // Before an op overwrites every element of `o` without reading it: views
 // and products still pending on o's block keep that block -- it moves to a
 // storage of their own -- and o's storage takes a fresh block from the
 // pool, so nothing is copied. (The executor rewrites its node buffers each
 // step while views of last step's values are still pending.)
 void move_aside(Tensor &o) {
+  if (!pending_norms().empty()) {
+    flush_norm(o.get_storage()->data());
+    flush_norms_reading(o.get_storage()->data());
+  }
   auto &views = pending_views();
   ResultCache &c = cache();
   auto *os = o.get_storage();
@@ -357,8 +428,17 @@ void move_aside(Tensor &o) {
   written(os->data());
 }
 
+// Runs the squared-norm collections that read block `base` (a gradient) or
+// accumulate into it, before its contents change.
+void settle_norms(const void *base) {
+  if (pending_norms().empty()) return;
+  flush_norm(base);
+  flush_norms_reading(base);
+}
+
 // Drops the pending view of block `base`, if any, without filling it.
 void drop_view(const void *base) {
+  settle_norms(base);
   auto &views = pending_views();
   const auto it = views.find(base);
   if (it == views.end()) return;
@@ -645,6 +725,7 @@ void Runtime::start() {
 void Runtime::submit() {
   State &s = *state_;
   if (!s.recording) throw std::logic_error("HIP runtime execution has not started");
+  while (!pending_norms().empty()) flush_norm(pending_norms().begin()->first);
   s.recording = false;
   s.submitted = true;
   if (!s.capturing) return;
@@ -754,6 +835,7 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   // reads a block that is itself a pending view.)
   auto &views = pending_views();
   const void *ob_ = o.get_storage() ? static_cast<const void *>(o.get_storage()->data()) : nullptr;
+  if (ob_) settle_norms(ob_); // (before the lookup: it may fill views)
   const auto self = ob_ ? views.find(ob_) : views.end();
   const bool same_a = a.get_storage() == o.get_storage(), same_b = b.get_storage() == o.get_storage();
   if (self != views.end() && !self->second.product && (same_a || same_b) &&
@@ -1321,13 +1403,19 @@ void Runtime::accumulate_gradient_squared_norm(const Tensor &g, Tensor &s) {
   if (s.numel() != 1) throw std::invalid_argument("gradient norm destination must be a scalar");
   note(kSquaredNorm, g.shape());
   if (g.numel() == 0) return;
-  float *acc = out(s);
-  // a gradient slot still holding a copy of its one contribution
-  // (context.h:73-89) is read at the copy's source
-  const PendingView *v = view_of(g);
-  const float *src = v && v->strides == g.strides() ? v->source.get_storage()->data() : in(g);
-  check(tlh_accumulate_gradient_squared_norm(src, g.numel(), acc, stream()),
-        "accumulate_gradient_squared_norm");
+  // collected (see pending_norms): the first call fills whatever reads or is
+  // pending on s, later ones only give s a new value identity
+  auto &norms = pending_norms();
+  const void *sb = s.get_storage()->data();
+  auto it = norms.find(sb);
+  if (it == norms.end()) {
+    out(s);
+    it = norms.emplace(sb, PendingNorm{s, {}}).first;
+  } else {
+    written(sb);
+  }
+  it->second.grads.push_back(g);
+  if (it->second.grads.size() >= 2048) flush_norm(sb); // the multi-tensor kernel's limit
 }
 
 void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_norm, Tensor &o) {
@@ -1339,6 +1427,9 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
     throw std::invalid_argument("maximum gradient norm must be finite and positive");
   note(kClip, g.shape());
   if (g.numel() == 0) return;
+  // the norm first: its collection may read g's pending view
+  if (s.get_storage()) settle_norms(s.get_storage()->data());
+  if (o.get_storage()) settle_norms(o.get_storage()->data());
   // in place on a slot that still holds a copy: read the copy's source and
   // write every element of the slot, so the copy is never made
   if (const PendingView *v = view_of(g);

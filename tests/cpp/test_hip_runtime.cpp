@@ -840,6 +840,36 @@ void repeated_results(hip::Runtime &rt) {
   }
 }
 
+// Squared norms accumulated into one scalar are collected and run together
+// (Compiled::step(max_norm), include/passes/compile.h:241-245): the scalar
+// keeps its starting value, a gradient written after its accumulation still
+// counts with its old values, and host reads and later ops see the sum.
+void collected_norms(hip::Runtime &rt) {
+  Tensor a({3}), b({2, 2}), c({1}), s({1}), t({1}), scaled({2, 2});
+  fill(a, {1, 2, 3});       // 14
+  fill(b, {1, 1, 1, 1});    // 4
+  fill(c, {5});             // 25
+  fill(s, {100});
+  fill(t, {0});
+  run(rt, [&] {
+    rt.accumulate_gradient_squared_norm(a, s);
+    rt.accumulate_gradient_squared_norm(b, s);
+    rt.add(b, b, b);        // b = 2: written after its accumulation
+    rt.accumulate_gradient_squared_norm(c, t);
+    rt.accumulate_gradient_squared_norm(b, t); // 25 + 16
+    rt.divide(b, s, scaled); // reads s: 2 / 118
+  });
+  expect(s, {118});
+  expect(t, {41});
+  expect(scaled, {2.0f / 118, 2.0f / 118, 2.0f / 118, 2.0f / 118});
+  // collected at submit, then read by the host
+  run(rt, [&] {
+    rt.accumulate_gradient_squared_norm(c, s);
+    rt.accumulate_gradient_squared_norm(c, s);
+  });
+  expect(s, {168});
+}
+
 // A per-entry weight gradient as the executor forms it
 // (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
 // input, a batched product with the output gradient, then sum_to_shape over
@@ -1030,6 +1060,7 @@ int main(int argc, char **argv) {
     harness::run("deferred_views", [&] { deferred_views(rt); });
     harness::run("deferred_products", [&] { deferred_products(rt); });
     harness::run("repeated_results", [&] { repeated_results(rt); });
+    harness::run("collected_norms", [&] { collected_norms(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
