@@ -257,8 +257,33 @@ std::unordered_map<const void *, PendingNorm> &pending_norms() {
 void flush_norm(const void *s_block);           // the collection into this scalar, if any
 void flush_norms_reading(const void *block);    // every collection holding this gradient
 
+// ---- AdamW updates collected ---------------------------------------------------
+// exec::step updates every parameter with its own adamW call (the
+// optimiser's update, include/optimiser/AdamW.h); in-place updates that share
+// the hyper-parameter scalars are collected and run as one multi-tensor
+// launch at submit(), or before anything reads or writes a parameter or
+// moment they update, or writes a gradient or scalar they read.
+struct AdamEntry {
+  Tensor p, g, m1, m2;
+  uint32_t step;
+};
+struct PendingAdam {
+  std::vector<AdamEntry> entries;
+  Tensor beta1, beta2, decay, lr;
+  float eps = 0.0f;
+  std::unordered_map<const void *, int> writes, reads; // blocks -> uses
+};
+PendingAdam &pending_adam() {
+  static auto *adam = new PendingAdam();
+  return *adam;
+}
+bool adam_pending() { return !pending_adam().entries.empty(); }
+void flush_adam();
+void settle(const void *base); // runs collected work that reads or writes this block
+
 // Before a kernel or the host reads block `base`.
 void reading(const void *base) {
+  if (adam_pending() && pending_adam().writes.count(base)) flush_adam();
   if (!pending_norms().empty()) flush_norm(base);
   if (!pending_views().empty()) materialise(base);
 }
@@ -267,6 +292,8 @@ void reading(const void *base) {
 // first (partial and in-place writes keep the rest), then every view whose
 // source is this block, which needs its current contents.
 void writing(const void *base) {
+  if (adam_pending() && (pending_adam().writes.count(base) || pending_adam().reads.count(base)))
+    flush_adam();
   if (!pending_norms().empty()) {
     flush_norm(base);
     flush_norms_reading(base);
@@ -288,6 +315,8 @@ void storage_hook(const void *base, int kind) {
     pending_views().clear();
     auto dead_norms = std::move(pending_norms());
     pending_norms().clear();
+    PendingAdam dead_adam = std::move(pending_adam());
+    pending_adam() = PendingAdam{};
     auto dead_results = std::move(cache().entries);
     cache().entries.clear();
     cache().ages.clear();
@@ -370,6 +399,37 @@ void flush_norm(const void *s_block) {
         "accumulate_gradient_squared_norm");
 }
 
+void flush_adam() {
+  PendingAdam pa = std::move(pending_adam());
+  pending_adam() = PendingAdam{};
+  const size_t n = pa.entries.size();
+  if (n == 0) return;
+  // device tables: p, g, m1, m2 pointers and sizes (u64 each), steps (u32)
+  std::vector<uint64_t> table(5 * n + (n + 1) / 2, 0);
+  uint32_t *steps = reinterpret_cast<uint32_t *>(table.data() + 5 * n);
+  for (size_t i = 0; i < n; ++i) {
+    AdamEntry &e = pa.entries[i];
+    table[i] = reinterpret_cast<uintptr_t>(e.p.get_storage()->data());
+    table[n + i] = reinterpret_cast<uintptr_t>(in(e.g));
+    table[2 * n + i] = reinterpret_cast<uintptr_t>(e.m1.get_storage()->data());
+    table[3 * n + i] = reinterpret_cast<uintptr_t>(e.m2.get_storage()->data());
+    table[4 * n + i] = e.p.numel();
+    steps[i] = e.step;
+  }
+  const size_t floats = 2 * table.size();
+  Tensor tables({uint32_t(floats)});
+  tables.get_storage()->write(
+      std::span<const float>(reinterpret_cast<const float *>(table.data()), floats), 0);
+  const float *t = in(tables);
+  const auto ptrs = [&](size_t k) { return reinterpret_cast<float *const *>(t + 2 * k * n); };
+  check(tlh_adamw_multi(ptrs(0), reinterpret_cast<const float *const *>(ptrs(1)), ptrs(2), ptrs(3),
+                        reinterpret_cast<const uint64_t *>(t + 8 * n),
+                        reinterpret_cast<const uint32_t *>(t + 10 * n), uint32_t(n),
+                        in(pa.beta1), in(pa.beta2), in(pa.decay), in(pa.lr), pa.eps, nullptr,
+                        0.0f, stream()),
+        "adamW");
+}
+
 void flush_norms_reading(const void *block) {
   std::vector<const void *> hits;
   for (const auto &[sb, pn] : pending_norms())
@@ -387,10 +447,7 @@ void flush_norms_reading(const void *block) {
 // pool, so nothing is copied. (The executor rewrites its node buffers each
 // step while views of last step's values are still pending.)
 void move_aside(Tensor &o) {
-  if (!pending_norms().empty()) {
-    flush_norm(o.get_storage()->data());
-    flush_norms_reading(o.get_storage()->data());
-  }
+  settle(o.get_storage()->data());
   auto &views = pending_views();
   ResultCache &c = cache();
   auto *os = o.get_storage();
@@ -428,9 +485,12 @@ void move_aside(Tensor &o) {
   written(os->data());
 }
 
-// Runs the squared-norm collections that read block `base` (a gradient) or
-// accumulate into it, before its contents change.
-void settle_norms(const void *base) {
+// Runs the collected work that reads block `base` or writes it (squared
+// norms of or into it, AdamW updates of or from it), before its contents
+// change.
+void settle(const void *base) {
+  if (adam_pending() && (pending_adam().writes.count(base) || pending_adam().reads.count(base)))
+    flush_adam();
   if (pending_norms().empty()) return;
   flush_norm(base);
   flush_norms_reading(base);
@@ -438,7 +498,7 @@ void settle_norms(const void *base) {
 
 // Drops the pending view of block `base`, if any, without filling it.
 void drop_view(const void *base) {
-  settle_norms(base);
+  settle(base);
   auto &views = pending_views();
   const auto it = views.find(base);
   if (it == views.end()) return;
@@ -726,6 +786,7 @@ void Runtime::submit() {
   State &s = *state_;
   if (!s.recording) throw std::logic_error("HIP runtime execution has not started");
   while (!pending_norms().empty()) flush_norm(pending_norms().begin()->first);
+  flush_adam();
   s.recording = false;
   s.submitted = true;
   if (!s.capturing) return;
@@ -835,7 +896,7 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   // reads a block that is itself a pending view.)
   auto &views = pending_views();
   const void *ob_ = o.get_storage() ? static_cast<const void *>(o.get_storage()->data()) : nullptr;
-  if (ob_) settle_norms(ob_); // (before the lookup: it may fill views)
+  if (ob_) settle(ob_); // (before the lookup: it may fill views)
   const auto self = ob_ ? views.find(ob_) : views.end();
   const bool same_a = a.get_storage() == o.get_storage(), same_b = b.get_storage() == o.get_storage();
   if (self != views.end() && !self->second.product && (same_a || same_b) &&
@@ -1428,8 +1489,8 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
   note(kClip, g.shape());
   if (g.numel() == 0) return;
   // the norm first: its collection may read g's pending view
-  if (s.get_storage()) settle_norms(s.get_storage()->data());
-  if (o.get_storage()) settle_norms(o.get_storage()->data());
+  if (s.get_storage()) settle(s.get_storage()->data());
+  if (o.get_storage()) settle(o.get_storage()->data());
   // in place on a slot that still holds a copy: read the copy's source and
   // write every element of the slot, so the copy is never made
   if (const PendingView *v = view_of(g);
@@ -1458,6 +1519,40 @@ void Runtime::adamW(const Tensor &p, const Tensor &g, Tensor &o, Tensor &m1, Ten
   if (step == 0) throw std::invalid_argument("AdamW step must be greater than zero");
   note(kAdamW, p.shape());
   if (p.numel() == 0) return;
+  const auto *bs1 = beta1.get_storage(), *bs2 = beta2.get_storage();
+  const auto *ds = decay.get_storage(), *ls = lr.get_storage();
+  if (o.get_storage() == p.get_storage() && bs1 && bs2 && ds && ls) {
+    // in place: collected (see pending_adam)
+    PendingAdam &pa = pending_adam();
+    if (adam_pending() && (pa.beta1.get_storage() != bs1 || pa.beta2.get_storage() != bs2 ||
+                           pa.decay.get_storage() != ds || pa.lr.get_storage() != ls ||
+                           pa.eps != epsilon))
+      flush_adam();
+    out(o); // fills what is pending on the blocks the update writes
+    out(m1);
+    out(m2);
+    PendingAdam &group = pending_adam(); // (the writes above may have run a group)
+    if (!adam_pending()) {
+      group.beta1 = beta1;
+      group.beta2 = beta2;
+      group.decay = decay;
+      group.lr = lr;
+      group.eps = epsilon;
+    }
+    group.entries.push_back(AdamEntry{p, g, m1, m2, step});
+    for (const void *b : {static_cast<const void *>(p.get_storage()->data()),
+                          static_cast<const void *>(m1.get_storage()->data()),
+                          static_cast<const void *>(m2.get_storage()->data())})
+      ++group.writes[b];
+    for (const void *b : {static_cast<const void *>(g.get_storage()->data()),
+                          static_cast<const void *>(bs1->data()),
+                          static_cast<const void *>(bs2->data()),
+                          static_cast<const void *>(ds->data()),
+                          static_cast<const void *>(ls->data())})
+      ++group.reads[b];
+    if (group.entries.size() >= 2048) flush_adam(); // the multi-tensor kernel's limit
+    return;
+  }
   float *po = out(o), *pm1 = out(m1), *pm2 = out(m2);
   check(tlh_adamw(in(p), in(g), po, pm1, pm2, in(beta1), in(beta2), in(decay), in(lr),
                   epsilon, step, p.numel(), stream()),

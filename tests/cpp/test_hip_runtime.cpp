@@ -870,6 +870,49 @@ void collected_norms(hip::Runtime &rt) {
   expect(s, {168});
 }
 
+// In-place AdamW updates are collected and run as one multi-tensor launch
+// (exec::step's per-parameter update calls): the same values as the
+// per-tensor kernel, a read of a parameter in between and a write to a
+// gradient after its update was queued see the right values.
+void collected_adamw(hip::Runtime &rt) {
+  Tensor b1({1}), b2({1}), dec({1}), lr({1});
+  fill(b1, {0.9f});
+  fill(b2, {0.999f});
+  fill(dec, {1.0f - 0.01f * 0.1f});
+  fill(lr, {0.01f});
+  const std::vector<uint32_t> sizes = {4, 7, 5};
+  std::vector<Tensor> p, g, m1, m2, q, qo, n1, n2;
+  for (size_t i = 0; i < sizes.size(); ++i) {
+    const uint32_t n = sizes[i];
+    const auto pv = random_values(n, 40 + uint32_t(i)), gv = random_values(n, 50 + uint32_t(i));
+    for (auto *v : {&p, &q}) v->emplace_back(std::vector<uint32_t>{n}).set(std::span<const float>(pv));
+    g.emplace_back(std::vector<uint32_t>{n}).set(std::span<const float>(gv));
+    for (auto *v : {&m1, &m2, &n1, &n2}) v->push_back(Tensor::from_zeros({n}));
+    qo.emplace_back(std::vector<uint32_t>{n});
+  }
+  Tensor peek({7});
+  for (uint32_t step = 1; step <= 2; ++step) {
+    run(rt, [&] {
+      for (size_t i = 0; i < sizes.size(); ++i) {
+        rt.adamW(p[i], g[i], p[i], m1[i], m2[i], b1, b2, dec, lr, 1e-8f, step); // collected
+        rt.adamW(q[i], g[i], qo[i], n1[i], n2[i], b1, b2, dec, lr, 1e-8f, step); // direct
+      }
+      rt.copy(p[1], peek);    // reads an updated parameter
+      rt.add(g[0], g[0], g[0]); // writes a gradient an update reads
+      for (size_t i = 0; i < sizes.size(); ++i) rt.copy(qo[i], q[i]);
+    });
+    for (size_t i = 0; i < sizes.size(); ++i) {
+      const auto a = host(p[i]), b = host(q[i]), ma = host(m1[i]), mb = host(n1[i]);
+      for (size_t j = 0; j < a.size(); ++j) {
+        CHECK_NEAR(a[j], b[j], 1e-6);
+        CHECK_NEAR(ma[j], mb[j], 1e-6);
+      }
+    }
+    const auto pk = host(peek), p1 = host(p[1]);
+    for (size_t j = 0; j < 7; ++j) CHECK(pk[j] == p1[j]);
+  }
+}
+
 // A per-entry weight gradient as the executor forms it
 // (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
 // input, a batched product with the output gradient, then sum_to_shape over
@@ -1061,6 +1104,7 @@ int main(int argc, char **argv) {
     harness::run("deferred_products", [&] { deferred_products(rt); });
     harness::run("repeated_results", [&] { repeated_results(rt); });
     harness::run("collected_norms", [&] { collected_norms(rt); });
+    harness::run("collected_adamw", [&] { collected_adamw(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
