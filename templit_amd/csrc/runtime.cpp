@@ -831,6 +831,23 @@ void Runtime::wait() {
   check(tlh_stream_synchronize(stream()), "HIP runtime execution");
 }
 
+namespace {
+void forget_recorded_work() noexcept {
+  ResultCache &c = cache();
+  auto dead_results = std::move(c.entries);
+  c.entries.clear();
+  c.ages.clear();
+  c.blocks.clear();
+  c.derived.clear();
+  c.bytes = 0;
+  block_values().clear(); // every block takes a fresh identity on next use
+  auto dead_norms = std::move(pending_norms());
+  pending_norms().clear();
+  PendingAdam dead_adam = std::move(pending_adam());
+  pending_adam() = PendingAdam{};
+}
+} // namespace
+
 void Runtime::abort() noexcept {
   State &s = *state_;
   if (s.capturing) {
@@ -838,10 +855,15 @@ void Runtime::abort() noexcept {
     if (tlh_graph_end_capture_graph(stream(), &graph) == 0) tlh_graph_free(graph);
     hip::detail::defer_releases(false); // the dropped graph never runs
     s.capturing = false;
+    // Nothing recorded in the dropped graph ran: cached results and value
+    // identities may name blocks it was to write, and the collected norm and
+    // AdamW calls belong to it.
+    forget_recorded_work();
   }
   s.recording = false;
   s.submitted = false;
 }
+
 
 void Runtime::cleanup() noexcept {
   if (!state_) return;

@@ -870,6 +870,27 @@ void collected_norms(hip::Runtime &rt) {
   expect(s, {168});
 }
 
+// A graph-mode recording that is aborted never runs: a later identical op
+// must compute its result, not take the dropped graph's as done, and
+// collected optimiser calls of the aborted phase are dropped with it.
+void aborted_capture_forgets_results(hip::Runtime &rt) {
+  Tensor a({2, 3}), b({3, 2}), o({2, 2}), s({1}), g({3});
+  fill(a, {1, 2, 3, 4, 5, 6});
+  fill(b, {7, 8, 9, 10, 11, 12});
+  fill(o, {0, 0, 0, 0});
+  fill(s, {1});
+  fill(g, {1, 1, 1});
+  rt.set_graph_mode(true);
+  rt.start();
+  rt.mult(a, b, o);
+  rt.accumulate_gradient_squared_norm(g, s);
+  rt.abort();
+  rt.set_graph_mode(false);
+  run(rt, [&] { rt.mult(a, b, o); });
+  expect(o, {58, 64, 139, 154});
+  expect(s, {1});
+}
+
 // In-place AdamW updates are collected and run as one multi-tensor launch
 // (exec::step's per-parameter update calls): the same values as the
 // per-tensor kernel, a read of a parameter in between and a write to a
@@ -1105,6 +1126,8 @@ int main(int argc, char **argv) {
     harness::run("repeated_results", [&] { repeated_results(rt); });
     harness::run("collected_norms", [&] { collected_norms(rt); });
     harness::run("collected_adamw", [&] { collected_adamw(rt); });
+    harness::run("aborted_capture_forgets_results",
+                 [&] { aborted_capture_forgets_results(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
     harness::run("storage_semantics", [&] { storage_semantics(rt); });
   }
