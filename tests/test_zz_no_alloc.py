@@ -72,15 +72,17 @@ def test_noalloc_matches_workspace_form_on_consecutive_calls(g, first, second):
 
 
 def test_noalloc_refuses_products_beyond_its_scratch(g):
-    # 3456 x 4352 on 128x128 tiles: 918 tiles on 256 CUs, so 150 tail
-    # tiles are cut into 16 K chunks, 39.3 M floats of partials: more than
-    # the array holds. The call returns an error and writes nothing.
+    # A^T.B with A stored [K, M], 3456 x 4352 on 128x128 tiles: 918 tiles on
+    # 256 CUs, so 150 tail tiles are cut into 16 K chunks, 39.3 M floats of
+    # partials: more than the array holds. The call returns an error and
+    # writes nothing.
     M, K, N = 3456, 1024, 4352
-    n = workspace_elems(g, M, K, N)
-    assert n > SCRATCH_FLOATS
-    a, b = g.zeros((M, K)), g.zeros((K, N))
+    ta = (M, K, N, 1, M, N, 1, N, 1, 0, u32([1]), u32([0]), u32([0]), u32([0]))
+    n = ctypes.c_size_t()
+    check(g.lib.tlh_matmul_workspace_size(*ta, ctypes.byref(n)), "workspace_size")
+    assert n.value > SCRATCH_FLOATS
+    a, b = g.zeros((K, M)), g.zeros((K, N))
     out = g.dev(np.full((M, N), 7.0, np.float32))
-    st = g.lib.tlh_matmul_noalloc(a.data_ptr(), b.data_ptr(), out.data_ptr(), *args(M, K, N),
-                                  g.stream)
+    st = g.lib.tlh_matmul_noalloc(a.data_ptr(), b.data_ptr(), out.data_ptr(), *ta, g.stream)
     assert st != 0
     assert np.all(g.host(out) == 7.0)
