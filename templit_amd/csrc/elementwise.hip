@@ -298,6 +298,32 @@ __global__ __launch_bounds__(256) void transpose_tiled_kernel(const float *__res
                  ld_in, blockIdx.y * 64, blockIdx.x * 64, tile);
 }
 
+// The same tiles for any permutation whose input is contiguous along the
+// output's second-to-last dim: out[z, i, j] = a[off(z) + j*ld_in + i], the
+// batch entry z's input offset from its coordinates in the leading output
+// dims (composed views: the K^T of a head-split projection, [B,H,64,T] read
+// from [B,T,H,64]).
+struct BatchDims {
+  int n;
+  uint32_t shape[kMaxDims];
+  uint32_t stride[kMaxDims];
+};
+__global__ __launch_bounds__(256) void transpose_batched_kernel(const float *__restrict__ a,
+                                                                float *__restrict__ out,
+                                                                uint32_t rows, uint32_t cols,
+                                                                uint32_t ld_in, BatchDims B) {
+  __shared__ float tile[64][65];
+  uint32_t rem = blockIdx.z;
+  size_t off = 0;
+  for (int d = B.n - 1; d >= 0; --d) {
+    const uint32_t c = rem % B.shape[d];
+    rem /= B.shape[d];
+    off += size_t(c) * B.stride[d];
+  }
+  transpose_tile(a + off, out + size_t(blockIdx.z) * rows * cols, rows, cols, ld_in,
+                 blockIdx.y * 64, blockIdx.x * 64, tile);
+}
+
 // Block b handles output tile b - first_tile of the job whose tile range
 // holds b; the threads test one job each to find it. A block that no job
 // claims does nothing, and transpose_tile keeps every access inside the
@@ -408,14 +434,35 @@ TLH_API int tlh_transpose_multi(const float *src, float *dst, const tlh_transpos
   return launch_status();
 }
 
-TLH_API int tlh_transpose(const float *a, float *out, uint32_t ndim, const uint32_t *out_shape,
-                          const uint32_t *in_strides, void *stream) {
-  if (ndim > kMaxDims || ndim == 0) return int(hipErrorInvalidValue);
+TLH_API int tlh_transpose(const float *a, float *out, uint32_t ndim_in,
+                          const uint32_t *out_shape_in, const uint32_t *in_strides_in,
+                          void *stream) {
+  if (ndim_in > kMaxDims || ndim_in == 0) return int(hipErrorInvalidValue);
   if (a == out) return int(hipErrorInvalidValue);
   size_t n = 1;
-  for (uint32_t d = 0; d < ndim; ++d) n *= out_shape[d];
+  for (uint32_t d = 0; d < ndim_in; ++d) n *= out_shape_in[d];
   if (n == 0) return 0;
   hipStream_t s = as_stream(stream);
+  // Size-1 dims dropped and adjacent output dims merged where the input
+  // walks them as one run (stride[d] = shape[d+1] * stride[d+1]): the same
+  // permutation with fewer dims, e.g. [B,T,H,D] <- [B,H,D,T] as [B,T,H*D].
+  uint32_t out_shape[kMaxDims], in_strides[kMaxDims], ndim = 0;
+  for (uint32_t d = 0; d < ndim_in; ++d) {
+    if (out_shape_in[d] == 1) continue;
+    if (ndim > 0 && in_strides[ndim - 1] == out_shape_in[d] * in_strides_in[d]) {
+      out_shape[ndim - 1] *= out_shape_in[d];
+      in_strides[ndim - 1] = in_strides_in[d];
+      continue;
+    }
+    out_shape[ndim] = out_shape_in[d];
+    in_strides[ndim] = in_strides_in[d];
+    ++ndim;
+  }
+  if (ndim == 0) { // a single element
+    out_shape[0] = 1;
+    in_strides[0] = 1;
+    ndim = 1;
+  }
   // Batched swap of the last two dims of a contiguous input: tiled path.
   if (ndim >= 2) {
     const uint32_t R = out_shape[ndim - 2], C = out_shape[ndim - 1];
@@ -429,6 +476,19 @@ TLH_API int tlh_transpose(const float *a, float *out, uint32_t ndim, const uint3
     if (last_two && batch <= 65535 && R > 1 && C > 1) {
       dim3 grid(ceil_div(C, 64), ceil_div(R, 64), unsigned(batch));
       transpose_tiled_kernel<<<grid, 256, 0, s>>>(a, out, R, C, size_t(R) * C, R);
+      return launch_status();
+    }
+    // any other layout whose input runs along the output's rows
+    if (in_strides[ndim - 2] == 1 && in_strides[ndim - 1] > 1 && batch <= 65535 && R > 1 &&
+        C > 1) {
+      BatchDims B{};
+      B.n = int(ndim) - 2;
+      for (uint32_t d = 0; d + 2 < ndim; ++d) {
+        B.shape[d] = out_shape[d];
+        B.stride[d] = in_strides[d];
+      }
+      dim3 grid(ceil_div(C, 64), ceil_div(R, 64), unsigned(batch));
+      transpose_batched_kernel<<<grid, 256, 0, s>>>(a, out, R, C, in_strides[ndim - 1], B);
       return launch_status();
     }
   }

@@ -113,6 +113,28 @@ def test_transpose(g, shape, da, db):
     np.testing.assert_array_equal(g.host(out), expect)  # a permutation is exact
 
 
+@pytest.mark.parametrize("shape,perm", [
+    ((4, 96, 6, 64), (0, 2, 3, 1)),    # K^T of a head split: [B,T,H,D] -> [B,H,D,T]
+    ((2, 70, 3, 33), (0, 2, 3, 1)),    # ragged tiles
+    ((5, 7, 9, 11), (2, 0, 3, 1)),     # leading dims permuted as well
+    ((4, 6, 64, 96), (0, 3, 1, 2)),    # head merge [B,H,D,T] -> [B,T,H,D]: H,D fold to one dim
+    ((3, 1, 40, 70), (0, 3, 1, 2)),    # a size-1 dim dropped
+    ((3, 64, 130), (2, 0, 1)),         # folds to a plain 2-D transpose
+    ((3, 64, 130), (2, 1, 0)),         # input-contiguous dim leading: the gather path
+])
+def test_transpose_general_permutations(g, shape, perm):
+    # adjacent output dims that the input walks as one run are folded
+    # together; permutations whose input is then contiguous along the
+    # output's second-to-last dim take the batched tiled kernel (the others
+    # a gather); every element moves exactly
+    x = O.normal(shape, 19)
+    expect = np.ascontiguousarray(np.transpose(x, perm))
+    ist = [O.contiguous_strides(shape)[p] for p in perm]
+    out = g.empty(expect.shape)
+    g.call("tlh_transpose", g.dev(x), out, len(shape), u32(expect.shape), u32(ist))
+    np.testing.assert_array_equal(g.host(out), expect)
+
+
 JOB = np.dtype([("src", "<u8"), ("dst", "<u8"), ("rows", "<u4"), ("cols", "<u4"),
                 ("first_tile", "<u4"), ("reserved", "<u4")])
 
