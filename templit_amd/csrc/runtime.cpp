@@ -23,6 +23,7 @@
 #include <list>
 #include <memory>
 #include <numeric>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -446,7 +447,7 @@ void flush_norms_reading(const void *block) {
 // storage of their own -- and o's storage takes a fresh block from the
 // pool, so nothing is copied. (The executor rewrites its node buffers each
 // step while views of last step's values are still pending.)
-void move_aside(Tensor &o) {
+std::optional<Tensor> move_aside(Tensor &o) {
   settle(o.get_storage()->data());
   auto &views = pending_views();
   ResultCache &c = cache();
@@ -459,8 +460,11 @@ void move_aside(Tensor &o) {
   const bool cached = c.blocks.count(base) > 0;
   if (!cached &&
       std::none_of(views.begin(), views.end(), [&](const auto &e) { return reads(e.second); }))
-    return;
-  if (os->size() == 0 || os->size() > UINT32_MAX) return writing(base);
+    return std::nullopt;
+  if (os->size() == 0 || os->size() > UINT32_MAX) {
+    writing(base);
+    return std::nullopt;
+  }
   // the readers (and cached results) are pointed at the new storage first,
   // then the blocks swap; the old block keeps its value identity
   Tensor holder({uint32_t(os->size())});
@@ -483,6 +487,7 @@ void move_aside(Tensor &o) {
   }
   os->exchange_block(*holder.get_storage());
   written(os->data());
+  return holder;
 }
 
 // Runs the collected work that reads block `base` or writes it (squared
@@ -575,6 +580,20 @@ void defer_reshape(const Tensor &a, Tensor &o) {
     reading(a.get_storage()->data());
   pending_views()[o.get_storage()->data()] = PendingView{std::move(source), o.shape(), o.strides()};
   set_value(o.get_storage()->data(), value_of(a.get_storage()->data()));
+}
+
+// True when block `base` holds a still valid cached result of an op other
+// than `op`. An in-place op of another kind that rewrote it would end a
+// chain of reusable results: the softmax derivative p * (g - rowsum(g * p))
+// is evaluated once per path through the scores, and each evaluation writes
+// the product over the difference it reads.
+bool holds_other_result(const void *base, uint32_t op) {
+  ResultCache &c = cache();
+  if (!c.blocks.count(base)) return false;
+  const ValueId v = value_of(base);
+  for (const auto &[key, e] : c.entries)
+    if (e.result.get_storage()->data() == base && e.value == v && key.words[0] != op) return true;
+  return false;
 }
 
 // The destination of an op that writes every element of `o`: unless one of
@@ -935,6 +954,24 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
     written(o.get_storage()->data());
     remember(std::move(key.key), o);
     return;
+  }
+  // An in-place op over a cached result of another op: the result keeps the
+  // old block, which the op reads, and o takes a fresh one (move_aside), so
+  // the next evaluation of the same expression still finds it.
+  if ((same_a || same_b) && ob_ && self == views.end() && holds_other_result(ob_, op) &&
+      (!same_a || (a.shape() == o.shape() && a.strides() == o.strides())) &&
+      (!same_b || (b.shape() == o.shape() && b.strides() == o.strides()))) {
+    if (const std::optional<Tensor> old = move_aside(o)) {
+      const Operand src{old->get_storage()->data(), o.strides(), &*old};
+      const Operand oa = same_a ? src : operand(a, false), ob = same_b ? src : operand(b, false);
+      const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
+      const auto sb = broadcast_strides(b.shape(), ob.strides, o.shape());
+      check(fn(oa.ptr, ob.ptr, out(o), uint32_t(o.shape().size()), o.shape().data(), sa.data(),
+               sb.data(), stream()),
+            what);
+      remember(std::move(key.key), o);
+      return;
+    }
   }
   // the destination first: views of it are filled before it is written
   float *dst = dest(o, {&a, &b});

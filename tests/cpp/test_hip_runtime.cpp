@@ -808,10 +808,10 @@ void repeated_results(hip::Runtime &rt) {
   Tensor p5({8, 4}), p6({8, 4}), p7({8, 4});
   run(rt, [&] {
     rt.mult(a, b, p5);
-    rt.add(p5, p5, p5); // in place: p5 = 2ab, the cached product is gone from it
-    rt.mult(a, b, p6);  // runs again
-    rt.exp(w, p6);      // p6 overwritten whole: the cached product moves aside
-    rt.mult(a, b, p7);  // reused from the moved block
+    rt.add(p5, p5, p5); // in place: p5 = 2ab; the cached product keeps the old block
+    rt.mult(a, b, p6);  // reused from that block
+    rt.exp(w, p6);      // p6 overwritten whole
+    rt.mult(a, b, p7);  // reused again
   });
   expect_prod(p5, av, bv, 2, 0);
   expect_prod(p7, av, bv, 1, 0);
@@ -837,6 +837,33 @@ void repeated_results(hip::Runtime &rt) {
       for (size_t j = 0; j < 4; ++j)
         CHECK_NEAR(gr[i * 4 + j], std::exp(prod(av, bv, i, j) - mx) / z, 1e-5);
     }
+  }
+  // 5. an expression evaluated once per path, whose evaluation writes a
+  // product in place over a difference it just computed (the softmax
+  // derivative p * (g - m)): the difference stays cached in its own block,
+  // later evaluations reuse it, and each product sees the difference
+  Tensor g({8, 4}), m({8, 1}), pw({8, 4}), d1({8, 4}), d2({8, 4}), d3({8, 4});
+  const std::vector<float> gv = random_values(32, 33), mv = random_values(8, 34),
+                           pv = random_values(32, 35);
+  g.set(std::span<const float>(gv));
+  m.set(std::span<const float>(mv));
+  pw.set(std::span<const float>(pv));
+  run(rt, [&] {
+    rt.sub(g, m, d1);
+    rt.hadamard(pw, d1, d1); // in place over the cached difference
+    rt.sub(g, m, d2);        // reused
+    rt.hadamard(pw, d2, d2); // reused as well: the same inputs again
+    rt.sub(g, m, d3);
+  });
+  {
+    const auto h1 = host(d1), h2 = host(d2), h3 = host(d3);
+    for (size_t i = 0; i < 8; ++i)
+      for (size_t j = 0; j < 4; ++j) {
+        const float diff = gv[i * 4 + j] - mv[i];
+        CHECK(h3[i * 4 + j] == diff);
+        CHECK(h1[i * 4 + j] == pv[i * 4 + j] * diff);
+        CHECK(h2[i * 4 + j] == h1[i * 4 + j]);
+      }
   }
 }
 
