@@ -984,11 +984,28 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   remember(std::move(key.key), o);
 }
 
+// For an op on one input that rewrites o in place (a is o) while o's block
+// holds a cached result of another op (the executor's
+// divide(mean, D, mean) after the sum that produced mean): the result moves
+// aside, and the returned block holding it is what the op reads.
+std::optional<Tensor> in_place_aside(const Tensor &a, Tensor &o, uint32_t op) {
+  if (a.get_storage() != o.get_storage() || !o.get_storage()) return std::nullopt;
+  const void *base = o.get_storage()->data();
+  if (pending_views().count(base) || !holds_other_result(base, op)) return std::nullopt;
+  return move_aside(o);
+}
+
 void unary(const Tensor &a, Tensor &o, UnaryFn fn, const char *what, uint32_t op) {
   require_same_count(a, o, what);
   if (o.numel() == 0) return;
   KeyBuilder key(op);
   key.tensor(a).dims(o.shape());
+  if (reuse(key.key, o)) return;
+  if (const std::optional<Tensor> old = in_place_aside(a, o, op)) {
+    check(fn(old->get_storage()->data(), out(o), o.numel(), stream()), what);
+    remember(std::move(key.key), o);
+    return;
+  }
   cached(key, o, {&a}, [&](float *dst) { check(fn(in(a), dst, o.numel(), stream()), what); });
 }
 
@@ -998,6 +1015,12 @@ void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *wha
   if (o.numel() == 0) return;
   KeyBuilder key(op);
   key.tensor(a).scalar(v);
+  if (reuse(key.key, o)) return;
+  if (const std::optional<Tensor> old = in_place_aside(a, o, op)) {
+    check(fn(old->get_storage()->data(), v, out(o), o.numel(), stream()), what);
+    remember(std::move(key.key), o);
+    return;
+  }
   cached(key, o, {&a}, [&](float *dst) { check(fn(in(a), v, dst, o.numel(), stream()), what); });
 }
 } // namespace

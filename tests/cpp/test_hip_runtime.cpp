@@ -865,6 +865,23 @@ void repeated_results(hip::Runtime &rt) {
         CHECK(h2[i * 4 + j] == h1[i * 4 + j]);
       }
   }
+  // 6. the same for an op on one input: a row sum divided in place (the
+  // RMSNorm derivative's mean, execute.h:343-348), then the sum again
+  Tensor m1({8, 1}), m2({8, 1});
+  run(rt, [&] {
+    rt.sum_to_shape(g, std::vector<uint32_t>{8, 1}, m1);
+    rt.divide(m1, 4.0f, m1); // in place over the cached sum
+    rt.sum_to_shape(g, std::vector<uint32_t>{8, 1}, m2); // reused
+  });
+  {
+    const auto h1 = host(m1), h2 = host(m2);
+    for (size_t i = 0; i < 8; ++i) {
+      double e = 0;
+      for (size_t j = 0; j < 4; ++j) e += gv[i * 4 + j];
+      CHECK_NEAR(h2[i], e, 1e-5);
+      CHECK(h1[i] == h2[i] / 4.0f);
+    }
+  }
 }
 
 // Squared norms accumulated into one scalar are collected and run together
