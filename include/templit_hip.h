@@ -309,7 +309,8 @@ int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
 int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
 /* Tuning hook: force every following tlh_gemm / tlh_matmul to use a
  * bm x bn tile (64 or 128 each; or 96 x 96 with bk 32 (4 waves) or 64 (8
- * waves); or, with bm = 16, the 16x16x4 MFMA kernel at bn x bn, bn 64 or
+ * waves); or 96 x 64 with bk 32 (4 waves); or, with bm = 16, the 16x16x4
+ * MFMA kernel at bn x bn, bn 64 or
  * 128, bk 32), a K tile of bk (16 or 32) and, where a
  * workspace allows it, `splits` K splits; bm = bn = 0 restores the
  * automatic plan. Process-wide, for measurement sweeps. A forced split
@@ -320,7 +321,7 @@ int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
  * bk = -7 / -8 the one-row (GEMV) path off / on (default on), bk = -9 /
  * -10 the float4 split-K reduce over a (plane, entry) grid off / on
  * (default on; off runs the grid-stride reduce, same bits), bk = -11 /
- * -12 the planner's 96x96 tiles off / on (default on), bk = -13 / -14 the
+ * -12 the planner's 96x96 and 96x64 tiles off / on (default on), bk = -13 / -14 the
  * split-major XCD order of split-K and batched grids off / on (default on;
  * same bits), bk = -15 / -16 split weight gradients (A transposed, B not)
  * on the 16x16x4 kernel off / on (default on), bk = -17 / -18 products with

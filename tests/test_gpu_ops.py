@@ -444,11 +444,11 @@ def test_gemm_split_major_xcd_order(g, forced_plan, M, N, batch):
         assert_close(bg, O.sum_to_shape(dys[j], [N]), rtol=1e-4, atol=1e-3, what=f"db[{j}]")
 
 
-def _every_layout(g, forced_plan, bm, bn, bk):
+def _every_layout(g, forced_plan, bm, bn, bk, M=256):
     # A tile plan on a tile-aligned shape (the bounds-free path), every
     # operand layout, and the weight-gradient form with its bias gradient,
     # unsplit and split over K; then ragged edges (the bounds-checked path).
-    M, N, K = 256, 384, 512
+    N, K = 384, 512
     for ta in (False, True):
         for tb in (False, True):
             forced_plan(bm, bn, 1, bk)
@@ -486,6 +486,24 @@ def test_gemm_tile16_square_plans(g, forced_plan, tile):
     # interleaved subtiles (b64 / b128 LDS reads), and it carries the bias
     # gradient of the weight-gradient form.
     _every_layout(g, forced_plan, 16, tile, 32)
+
+
+def test_gemm_96x64_tiles(g, forced_plan):
+    # 96x64 tiles on the 16x16x4 kernel (4 waves of 48x32): every layout on a
+    # tile-aligned shape (288 = 3 x 96 rows), the weight-gradient form with
+    # its bias gradient, split over K, and ragged edges
+    _every_layout(g, forced_plan, 96, 64, 32, M=288)
+
+
+def test_gemm_matmul_bias_configuration(g):
+    # [768,384].[384,1536] + bias (the matmul + bias configuration): 192
+    # tiles of 96x64, one round on the CUs; against fp64
+    M, K, N = 768, 384, 1536
+    a, b = O.normal((M, K), 156, 0, 0.02), O.normal((K, N), 157, 0, 0.02)
+    bias = O.normal((N,), 158, 0, 0.02)
+    out, _ = gemm(g, a, b, False, False, bias=bias)
+    expect = a.astype(np.float64) @ b.astype(np.float64) + bias
+    assert_rel(out.reshape(M, N), expect, 1e-3, "matmul + bias")
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
