@@ -309,7 +309,7 @@ int tlh_gemm(const tlh_gemm_desc *desc, void *stream);
 int tlh_gemm_workspace_size(const tlh_gemm_desc *desc, size_t *elems);
 /* Tuning hook: force every following tlh_gemm / tlh_matmul to use a
  * bm x bn tile (64 or 128 each; or 96 x 96 with bk 32 (4 waves) or 64 (8
- * waves); or 96 x 64 with bk 32 (4 waves); or, with bm = 16, the 16x16x4
+ * waves); or 96 x 64 with bk 32 (4 waves) or 64 (8 waves); or, with bm = 16, the 16x16x4
  * MFMA kernel at bn x bn, bn 64 or
  * 128, bk 32), a K tile of bk (16 or 32) and, where a
  * workspace allows it, `splits` K splits; bm = bn = 0 restores the

@@ -1341,14 +1341,16 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
     const bool can_split = allow_split && one_dim;
     if (g_force_bm == 16) // 16x16 MFMA, square tiles of g_force_bn, K tile 32
       return {g_force_bn, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, 32, true};
-    if (g_force_bm == 96 && g_force_bn == 64) // 96x64 tiles on 4 waves
+    if (g_force_bm == 96 && g_force_bn == 64) { // 96x64 tiles
+      // 8 waves over K tiles of 64 (as 96x96 below), else 4 waves
+      if (g_force_bk == 64 && !d.bias_grad && (!d.sum_batches || d.K % 64 == 0))
+        return {96, 64, 1, 64};
       return {96, 64, can_split ? std::max(1, g_force_splits) : 1, 32};
+    }
     if (g_force_bm == 96) { // 16x16 MFMA tiles, no bias gradient
       if (d.bias_grad) return {64, 64, 1, 32};
-      // 8 waves over K tiles of 64 (split-K chunks of 64 | chunk), summed
-      // entries of 64 | K
-      if (g_force_bk == 64 && (!d.sum_batches || d.K % 64 == 0))
-        return {96, 96, can_split ? std::max(1, g_force_splits) : 1, 64};
+      // 8 waves over K tiles of 64: no split-K, summed entries of 64 | K
+      if (g_force_bk == 64 && (!d.sum_batches || d.K % 64 == 0)) return {96, 96, 1, 64};
       return {96, 96, can_split ? std::max(1, g_force_splits) : 1, 32};
     }
     return {g_force_bm, g_force_bn, can_split ? std::max(1, g_force_splits) : 1, g_force_bk};
@@ -1372,14 +1374,16 @@ Plan make_plan(const GemmDesc &d, bool allow_split) {
   }
   // 96x64 tiles where they cover the output in 3/4 to 1 tile per CU and
   // 64x64 tiles would give some CUs a second one: [768,384].[384,1536]
-  // (matmul + bias at batch 4 x 192) is 192 tiles instead of 288, 19.8 ->
-  // 17.9 us (4 waves of 48x32; 6 accumulator chains each).
-  if (g_tile96 && !d.trans_a && vec_ok(d) && d.M % 96 == 0 && d.N % 64 == 0 && K % 32 == 0 &&
-      K >= 128) {
+  // (matmul + bias at batch 4 x 192) is 192 tiles instead of 288. With K
+  // tiles of 64 the block has 8 waves in two K groups (two waves per SIMD):
+  // 19.8 us on 64x64 tiles, 17.9 on 4-wave and 15.9 on 8-wave 96x64 tiles.
+  if (g_tile96 && !d.trans_a && !d.bias_grad && vec_ok(d) && d.M % 96 == 0 && d.N % 64 == 0 &&
+      K % 32 == 0 && K >= 128) {
     const size_t cus = size_t(cu_count());
     const size_t t = tiles_for(d, 96, 64) * outputs;
+    const bool k64 = K % 64 == 0 && (!d.sum_batches || d.K % 64 == 0);
     if (4 * t >= 3 * cus && t <= cus && tiles_for(d, 64, 64) * outputs > cus)
-      return {96, 64, 1, 32};
+      return {96, 64, 1, k64 ? 64 : 32};
   }
   // output area over the area of the tiles that cover it
   auto coverage = [&](int bm, int bn) {
@@ -1657,6 +1661,8 @@ int gemm_main(const Prepared &L, hipStream_t s) {
     launch16<64, 64, 32>(p, ta, tb, vec, full, grid, s);
   } else if (plan.m16 && plan.bm == 128) {
     launch16<128, 128, 32>(p, ta, tb, vec, full, grid, s);
+  } else if (plan.bm == 96 && plan.bn == 64 && plan.bk == 64) {
+    launch16x8<96, 64>(p, ta, tb, vec, full, grid, s);
   } else if (plan.bm == 96 && plan.bn == 64) {
     launch16<96, 64, 32>(p, ta, tb, vec, full, grid, s);
   } else if (plan.bm == 96 && plan.bk == 64) {
@@ -1806,7 +1812,7 @@ TLH_API int tlh_gemm_set_plan(int bm, int bn, int splits, int bk) {
     return 0;
   }
   const bool ok = (bm == 0 && bn == 0) || (bm == 96 && bn == 96 && (bk == 32 || bk == 64)) ||
-                  (bm == 96 && bn == 64 && bk == 32) ||
+                  (bm == 96 && bn == 64 && (bk == 32 || bk == 64)) ||
                   (bm == 16 && (bn == 64 || bn == 128) && bk == 32) ||
                   ((bm == 64 || bm == 128) && (bn == 64 || bn == 128));
   if (!ok || splits < 0 || splits > 64 || (bk != 16 && bk != 32 && (bk != 64 || bm != 96)))

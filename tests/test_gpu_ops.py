@@ -488,11 +488,13 @@ def test_gemm_tile16_square_plans(g, forced_plan, tile):
     _every_layout(g, forced_plan, 16, tile, 32)
 
 
-def test_gemm_96x64_tiles(g, forced_plan):
-    # 96x64 tiles on the 16x16x4 kernel (4 waves of 48x32): every layout on a
-    # tile-aligned shape (288 = 3 x 96 rows), the weight-gradient form with
-    # its bias gradient, split over K, and ragged edges
-    _every_layout(g, forced_plan, 96, 64, 32, M=288)
+@pytest.mark.parametrize("bk", [32, 64])
+def test_gemm_96x64_tiles(g, forced_plan, bk):
+    # 96x64 tiles on the 16x16x4 kernel (4 waves of 48x32, or 8 in two K
+    # groups): every layout on a tile-aligned shape (288 = 3 x 96 rows), the
+    # weight-gradient form with its bias gradient (4 waves), split over K,
+    # and ragged edges
+    _every_layout(g, forced_plan, 96, 64, bk, M=288)
 
 
 def test_gemm_matmul_bias_configuration(g):
@@ -691,15 +693,17 @@ def test_gemm_summed_batches(g, M, N, K):
     assert_rel(g.host(dc).reshape(M, N), expect, 1e-3, "summed")
 
 
+@pytest.mark.parametrize("bn", [96, 64])
 @pytest.mark.parametrize("bk", [32, 64])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
-def test_gemm_tile96(g, forced_plan, ta, tb, bk):
-    # 96x96 tiles on the 16x16x4 MFMA: every operand layout on the step's
-    # [6144,384] product (exactly 256 tiles), every epilogue, the head-layout
-    # store (96-column tiles straddle the 64-wide heads), the batched and
-    # summed-batch (K-segmented) forms and the bounds-checked ragged path.
-    # bk 32: 4 waves; bk 64: 8 waves in two K groups over K tiles of 64.
-    forced_plan(96, 96, 1, bk)
+def test_gemm_tile96(g, forced_plan, ta, tb, bk, bn):
+    # 96x96 and 96x64 tiles on the 16x16x4 MFMA: every operand layout on the
+    # step's [6144,384] product (exactly 256 tiles of 96x96), every epilogue,
+    # the head-layout store (96-column tiles straddle the 64-wide heads), the
+    # batched and summed-batch (K-segmented) forms and the bounds-checked
+    # ragged path. bk 32: 4 waves; bk 64: 8 waves in two K groups over K
+    # tiles of 64.
+    forced_plan(96, bn, 1, bk)
     M, N, K = 6144, 384, 384
     a = O.normal((K, M) if ta else (M, K), 180, 0, 0.5)
     b = O.normal((N, K) if tb else (K, N), 181, 0, 0.5)
@@ -728,9 +732,10 @@ def test_gemm_tile96(g, forced_plan, ta, tb, bk):
                "ragged")
 
 
+@pytest.mark.parametrize("bn", [96, 64])
 @pytest.mark.parametrize("bk", [32, 64])
-def test_gemm_tile96_batched_and_summed(g, forced_plan, bk):
-    forced_plan(96, 96, 1, bk)
+def test_gemm_tile96_batched_and_summed(g, forced_plan, bk, bn):
+    forced_plan(96, bn, 1, bk)
     M, N, K = 960, 192, 384
     a = O.normal((3, M, K), 187, 0, 0.5)
     w = O.normal((3, N, K), 188, 0, 0.5)
