@@ -146,7 +146,8 @@ struct MemoEntry {
 struct ResultCache {
   std::unordered_map<MemoKey, MemoEntry, MemoKeyHash> entries;
   std::list<MemoKey> ages;                        // most recent first
-  std::unordered_map<const void *, int> blocks;   // entries per result block
+  // the entries of each result block (pointers to their keys in `entries`)
+  std::unordered_map<const void *, std::vector<const MemoKey *>> blocks;
   std::unordered_map<MemoKey, ValueId, MemoKeyHash> derived; // transposed views
   size_t bytes = 0;
 };
@@ -190,7 +191,11 @@ void forget(std::unordered_map<MemoKey, MemoEntry, MemoKeyHash>::iterator it) {
   c.bytes -= it->second.bytes;
   c.ages.erase(it->second.age);
   const void *block = it->second.result.get_storage()->data();
-  if (--c.blocks[block] == 0) c.blocks.erase(block);
+  if (const auto b = c.blocks.find(block); b != c.blocks.end()) {
+    auto &keys = b->second;
+    keys.erase(std::remove(keys.begin(), keys.end(), &it->first), keys.end());
+    if (keys.empty()) c.blocks.erase(b);
+  }
   MemoEntry dead = std::move(it->second); // released after the erase
   c.entries.erase(it);
 }
@@ -478,10 +483,10 @@ std::optional<Tensor> move_aside(Tensor &o) {
   }
   if (cached) {
     std::vector<MemoKey> stale;
-    for (auto &[key, e] : c.entries) {
-      if (e.result.get_storage()->data() != base) continue;
+    for (const MemoKey *key : c.blocks.at(base)) {
+      MemoEntry &e = c.entries.find(*key)->second;
       if (e.result.numel() == os->size()) e.result = holder.view(e.result.shape());
-      else stale.push_back(key);
+      else stale.push_back(*key);
     }
     for (const MemoKey &key : stale) forget(c.entries.find(key));
   }
@@ -589,10 +594,11 @@ void defer_reshape(const Tensor &a, Tensor &o) {
 // the product over the difference it reads.
 bool holds_other_result(const void *base, uint32_t op) {
   ResultCache &c = cache();
-  if (!c.blocks.count(base)) return false;
+  const auto b = c.blocks.find(base);
+  if (b == c.blocks.end()) return false;
   const ValueId v = value_of(base);
-  for (const auto &[key, e] : c.entries)
-    if (e.result.get_storage()->data() == base && e.value == v && key.words[0] != op) return true;
+  for (const MemoKey *key : b->second)
+    if (c.entries.find(*key)->second.value == v && key->words[0] != op) return true;
   return false;
 }
 
@@ -643,8 +649,9 @@ void remember(MemoKey &&key, const Tensor &o) {
   if (const auto it = c.entries.find(key); it != c.entries.end()) forget(it);
   const void *block = o.get_storage()->data();
   c.ages.push_front(key);
-  c.entries.emplace(std::move(key), MemoEntry{value_of(block), o, bytes, c.ages.begin()});
-  ++c.blocks[block];
+  const auto it =
+      c.entries.emplace(std::move(key), MemoEntry{value_of(block), o, bytes, c.ages.begin()}).first;
+  c.blocks[block].push_back(&it->first);
   c.bytes += bytes;
   while (c.bytes > budget) forget(c.entries.find(c.ages.back()));
 }
