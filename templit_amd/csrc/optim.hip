@@ -30,6 +30,39 @@ __global__ __launch_bounds__(256) void clip_kernel(const float *__restrict__ g,
     out[i] = g[i] * scale;
 }
 
+constexpr uint32_t kClipChunk = 4096; // elements per work item (multiple of 4)
+
+// Multi-tensor in-place clip: work items are (tensor, 4096-element chunk)
+// pairs numbered across all tensors (a chunk map in LDS); block b takes
+// items b, b+G, ... . Each element is g * scale, as in clip_kernel.
+__global__ __launch_bounds__(256) void clip_multi_kernel(float *const *__restrict__ grads,
+                                                         const uint64_t *__restrict__ sizes,
+                                                         uint32_t count,
+                                                         const float *__restrict__ squared_norm,
+                                                         float max_norm) {
+  __shared__ uint32_t first[kMaxMultiTensors + 1];
+  const uint32_t total = build_chunk_map(
+      first, count, [&](uint32_t t) { return uint32_t((sizes[t] + kClipChunk - 1) / kClipChunk); });
+  const float scale = clip_scale(*squared_norm, max_norm);
+  for (uint32_t it = blockIdx.x; it < total; it += gridDim.x) {
+    const uint32_t t = chunk_owner(first, count, it);
+    const uint64_t n = sizes[t];
+    float *g = grads[t];
+    const uint64_t begin = uint64_t(it - first[t]) * kClipChunk;
+    const uint64_t end = begin + kClipChunk < n ? begin + kClipChunk : n;
+    if ((reinterpret_cast<uintptr_t>(g) & 15) == 0 && end - begin == kClipChunk) {
+      for (uint64_t i = begin + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
+        f4 v = *reinterpret_cast<const f4 *>(g + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = v[q] * scale;
+        *reinterpret_cast<f4 *>(g + i) = v;
+      }
+    } else {
+      for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) g[i] = g[i] * scale;
+    }
+  }
+}
+
 // One AdamW element update, in the operation order of math.metal:1008-1043.
 __device__ inline float adamw_update(float p, float g, float &m, float &v, float b1, float b2,
                                      float decay, float lr, float eps, float c1, float c2) {
@@ -125,6 +158,15 @@ TLH_API int tlh_clip_gradient(const float *g, const float *squared_norm, float m
   if (n == 0) return 0;
   clip_kernel<<<stride_grid(n, 256), 256, 0, as_stream(stream)>>>(g, squared_norm, max_norm, out,
                                                                   n);
+  return launch_status();
+}
+
+TLH_API int tlh_clip_multi(float *const *grads, const uint64_t *sizes, uint32_t count,
+                           const float *squared_norm, float max_norm, void *stream) {
+  if (count == 0) return 0;
+  if (count > kMaxMultiTensors || !squared_norm) return int(hipErrorInvalidValue);
+  clip_multi_kernel<<<1024, 256, 0, as_stream(stream)>>>(grads, sizes, count, squared_norm,
+                                                         max_norm);
   return launch_status();
 }
 

@@ -285,6 +285,23 @@ PendingAdam &pending_adam() {
 }
 bool adam_pending() { return !pending_adam().entries.empty(); }
 void flush_adam();
+
+// ---- in-place clips batched ---------------------------------------------------------
+// Compiled::step(max_norm) clips each gradient in place with a call of its
+// own (compile.h:246-249). Consecutive in-place clips by one norm and bound
+// are batched and run as one multi-tensor launch before the runtime does
+// anything else (the next op, a host access, submit), so every other
+// operation finds them done.
+struct ClipBatch {
+  std::vector<Tensor> grads;
+  Tensor s;
+  float max_norm = 0.0f;
+};
+ClipBatch &clip_batch() {
+  static auto *batch = new ClipBatch();
+  return *batch;
+}
+void flush_clips();
 void settle(const void *base); // runs collected work that reads or writes this block
 
 // Before a kernel or the host reads block `base`.
@@ -323,6 +340,8 @@ void storage_hook(const void *base, int kind) {
     pending_norms().clear();
     PendingAdam dead_adam = std::move(pending_adam());
     pending_adam() = PendingAdam{};
+    ClipBatch dead_clips = std::move(clip_batch());
+    clip_batch() = ClipBatch{};
     auto dead_results = std::move(cache().entries);
     cache().entries.clear();
     cache().ages.clear();
@@ -343,6 +362,7 @@ void storage_hook(const void *base, int kind) {
     views.erase(it);
     return;
   }
+  flush_clips(); // a host access sees them done
   if (kind == detail::kAccessRead) {
     reading(base);
   } else {
@@ -434,6 +454,27 @@ void flush_adam() {
                         in(pa.beta1), in(pa.beta2), in(pa.decay), in(pa.lr), pa.eps, nullptr,
                         0.0f, stream()),
         "adamW");
+}
+
+void flush_clips() {
+  if (clip_batch().grads.empty()) return;
+  ClipBatch b = std::move(clip_batch());
+  clip_batch() = ClipBatch{};
+  const size_t n = b.grads.size();
+  // device tables: gradient pointers, then element counts (u64 each)
+  std::vector<uint64_t> table(2 * n);
+  for (size_t i = 0; i < n; ++i) {
+    table[i] = reinterpret_cast<uintptr_t>(out(b.grads[i])); // readers of the old values first
+    table[n + i] = b.grads[i].numel();
+  }
+  Tensor tables({uint32_t(4 * n)});
+  tables.get_storage()->write(
+      std::span<const float>(reinterpret_cast<const float *>(table.data()), 4 * n), 0);
+  const float *t = in(tables);
+  check(tlh_clip_multi(reinterpret_cast<float *const *>(t),
+                       reinterpret_cast<const uint64_t *>(t + 2 * n), uint32_t(n), in(b.s),
+                       b.max_norm, stream()),
+        "clip_gradient");
 }
 
 void flush_norms_reading(const void *block) {
@@ -772,9 +813,10 @@ Runtime::Runtime() : state_(std::make_unique<State>()) {
 
 Runtime::~Runtime() { cleanup(); }
 
-void Runtime::require_recording(const char *op) const {
+void Runtime::require_recording(const char *op, bool run_clips) const {
   if (!state_->recording)
     throw std::logic_error(std::string("HIP runtime execution has not started (") + op + ")");
+  if (run_clips) flush_clips();
 }
 
 // FNV-1a over the op and its output shape: the key of a recorded sequence.
@@ -811,6 +853,7 @@ void Runtime::start() {
 void Runtime::submit() {
   State &s = *state_;
   if (!s.recording) throw std::logic_error("HIP runtime execution has not started");
+  flush_clips();
   while (!pending_norms().empty()) flush_norm(pending_norms().begin()->first);
   flush_adam();
   s.recording = false;
@@ -871,6 +914,8 @@ void forget_recorded_work() noexcept {
   pending_norms().clear();
   PendingAdam dead_adam = std::move(pending_adam());
   pending_adam() = PendingAdam{};
+  ClipBatch dead_clips = std::move(clip_batch());
+  clip_batch() = ClipBatch{};
 }
 } // namespace
 
@@ -1569,7 +1614,7 @@ void Runtime::accumulate_gradient_squared_norm(const Tensor &g, Tensor &s) {
 }
 
 void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_norm, Tensor &o) {
-  require_recording("clip_gradient");
+  require_recording("clip_gradient", false);
   if (s.numel() != 1) throw std::invalid_argument("gradient norm input must be a scalar");
   if (g.shape() != o.shape())
     throw std::invalid_argument("gradient clipping input and destination shapes must match");
@@ -1580,6 +1625,27 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
   // the norm first: its collection may read g's pending view
   if (s.get_storage()) settle(s.get_storage()->data());
   if (o.get_storage()) settle(o.get_storage()->data());
+  // in place on a materialised gradient: the clip joins the batch (see
+  // clip_batch); a gradient already in it, or another norm or bound, runs
+  // the batch first
+  if (g.get_storage() == o.get_storage() && g.strides() == o.strides() && s.get_storage() &&
+      !pending_views().count(g.get_storage()->data())) {
+    ClipBatch &cb = clip_batch();
+    bool fits = cb.grads.empty() ||
+                (cb.s.get_storage() == s.get_storage() && cb.max_norm == max_norm &&
+                 cb.grads.size() < 2048); // the multi-tensor kernel's limit
+    for (size_t i = 0; fits && i < cb.grads.size(); ++i)
+      fits = cb.grads[i].get_storage() != g.get_storage();
+    if (!fits) flush_clips();
+    ClipBatch &b = clip_batch();
+    if (b.grads.empty()) {
+      b.s = s;
+      b.max_norm = max_norm;
+    }
+    b.grads.push_back(g);
+    return;
+  }
+  flush_clips();
   // in place on a slot that still holds a copy: read the copy's source and
   // write every element of the slot, so the copy is never made
   if (const PendingView *v = view_of(g);

@@ -152,7 +152,9 @@ private:
   struct State;
   std::unique_ptr<State> state_;
 
-  void require_recording(const char *op) const;
+  // Throws unless recording; then runs the in-place clips batched so far
+  // (unless `run_clips` is false: another clip joins the batch).
+  void require_recording(const char *op, bool run_clips = true) const;
   void note(uint32_t op, std::span<const uint32_t> shape);
   void RMS_impl(const Tensor &a, Tensor &out);
   // sum_to_shape's reduction, `aligned` being the target right-aligned to

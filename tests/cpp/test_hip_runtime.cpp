@@ -978,6 +978,65 @@ void collected_adamw(hip::Runtime &rt) {
   }
 }
 
+// In-place clips by one norm are batched into one launch that runs before
+// anything else (Compiled::step(max_norm), include/passes/compile.h:246-249).
+// Checked against out-of-place clips, which run directly: the gradients, an
+// op reading one of them, a host read in the middle of the recording, a
+// gradient clipped twice and the AdamW updates that follow all agree.
+void batched_clips(hip::Runtime &rt) {
+  Tensor b1({1}), b2({1}), dec({1}), lr({1});
+  fill(b1, {0.9f});
+  fill(b2, {0.95f});
+  fill(dec, {1.0f - 0.01f * 0.1f});
+  fill(lr, {0.01f});
+  const std::vector<uint32_t> sizes = {4, 7, 4101}; // 4101: a partial chunk
+  std::vector<Tensor> p, g, m1, m2, q, h, hc, n1, n2, qo;
+  for (size_t i = 0; i < sizes.size(); ++i) {
+    const uint32_t n = sizes[i];
+    const auto pv = random_values(n, 80 + uint32_t(i));
+    auto gv = random_values(n, 90 + uint32_t(i));
+    for (auto &x : gv) x *= 3.0f; // a norm above the bound: the clip scales
+    for (auto *v : {&p, &q}) v->emplace_back(std::vector<uint32_t>{n}).set(std::span<const float>(pv));
+    for (auto *v : {&g, &h}) v->emplace_back(std::vector<uint32_t>{n}).set(std::span<const float>(gv));
+    for (auto *v : {&m1, &m2, &n1, &n2}) v->push_back(Tensor::from_zeros({n}));
+    hc.emplace_back(std::vector<uint32_t>{n});
+    qo.emplace_back(std::vector<uint32_t>{n});
+  }
+  Tensor s({1}), s2({1}), peek({7}), peek2({7});
+  fill(s, {0.0f});
+  fill(s2, {0.0f});
+  std::vector<float> mid;
+  run(rt, [&] {
+    for (size_t i = 0; i < sizes.size(); ++i) {
+      rt.accumulate_gradient_squared_norm(g[i], s);
+      rt.accumulate_gradient_squared_norm(h[i], s2);
+    }
+    for (size_t i = 0; i < sizes.size(); ++i) rt.clip_gradient(g[i], s, 1.0f, g[i]); // batched
+    for (size_t i = 0; i < sizes.size(); ++i) rt.clip_gradient(h[i], s2, 1.0f, hc[i]); // direct
+    mid = host(g[0]); // a host read runs the batch
+    rt.clip_gradient(g[2], s, 1.0f, g[2]);   // clipped twice: a new batch
+    rt.clip_gradient(hc[2], s2, 1.0f, hc[2]); // the same on the other side (another norm)
+    rt.copy(g[1], peek); // the op after the clips sees them done
+    rt.copy(hc[1], peek2);
+    for (size_t i = 0; i < sizes.size(); ++i) {
+      rt.adamW(p[i], g[i], p[i], m1[i], m2[i], b1, b2, dec, lr, 1e-8f, 1);
+      rt.adamW(q[i], hc[i], qo[i], n1[i], n2[i], b1, b2, dec, lr, 1e-8f, 1);
+    }
+    for (size_t i = 0; i < sizes.size(); ++i) rt.copy(qo[i], q[i]);
+  });
+  const auto hc0 = host(hc[0]);
+  for (size_t j = 0; j < hc0.size(); ++j) CHECK(mid[j] == hc0[j]);
+  for (size_t i = 0; i < sizes.size(); ++i) {
+    const auto ga = host(g[i]), gb = host(hc[i]), a = host(p[i]), b = host(q[i]);
+    for (size_t j = 0; j < ga.size(); ++j) {
+      CHECK(ga[j] == gb[j]); // the same clips of the same values
+      CHECK_NEAR(a[j], b[j], 1e-6); // and the updates (multi-tensor vs single kernel)
+    }
+  }
+  const auto k1 = host(peek), k2 = host(peek2);
+  for (size_t j = 0; j < 7; ++j) CHECK(k1[j] == k2[j]);
+}
+
 // A per-entry weight gradient as the executor forms it
 // (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
 // input, a batched product with the output gradient, then sum_to_shape over
@@ -1170,6 +1229,7 @@ int main(int argc, char **argv) {
     harness::run("repeated_results", [&] { repeated_results(rt); });
     harness::run("collected_norms", [&] { collected_norms(rt); });
     harness::run("collected_adamw", [&] { collected_adamw(rt); });
+    harness::run("batched_clips", [&] { batched_clips(rt); });
     harness::run("aborted_capture_forgets_results",
                  [&] { aborted_capture_forgets_results(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });
