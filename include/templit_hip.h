@@ -517,13 +517,14 @@ int tlh_attention_backward(const float *q, const float *k, const float *v,
  * sqrt(max(*squared_norm, 1e-12))). out may alias g. */
 int tlh_clip_gradient(const float *g, const float *squared_norm, float max_norm,
                       float *out, size_t n, void *stream);
-/* clip_gradient in place over `count` tensors in one launch: grads[i] (n =
- * sizes[i] elements) *= min(1, max_norm / sqrt(max(*squared_norm, 1e-12))),
- * the arithmetic of tlh_clip_gradient. No counterpart in the reference: it
- * serves Compiled::step(max_norm)'s per-gradient clip calls (compile.h:
- * 246-249), which hip::Runtime collects. Device arrays; count <= 2048. */
-int tlh_clip_multi(float *const *grads, const uint64_t *sizes, uint32_t count,
-                   const float *squared_norm, float max_norm, void *stream);
+/* clip_gradient over `count` tensors in one launch: dsts[i][j] = srcs[i][j]
+ * * min(1, max_norm / sqrt(max(*squared_norm, 1e-12))) for j < sizes[i],
+ * the arithmetic of tlh_clip_gradient; dsts[i] may be srcs[i], other
+ * tensors must not overlap. No counterpart in the reference: it serves
+ * Compiled::step(max_norm)'s per-gradient clip calls (compile.h:246-249),
+ * which hip::Runtime collects. Device arrays; count <= 2048. */
+int tlh_clip_multi(const float *const *srcs, float *const *dsts, const uint64_t *sizes,
+                   uint32_t count, const float *squared_norm, float max_norm, void *stream);
 /* adamW (math.metal:1008-1043, runtime.cpp:1129-1168): beta1, beta2, decay,
  * lr are 1-element device tensors (include/optimiser/AdamW.h:15-39). out may
  * alias param. step >= 1. */

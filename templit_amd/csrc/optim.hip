@@ -32,33 +32,37 @@ __global__ __launch_bounds__(256) void clip_kernel(const float *__restrict__ g,
 
 constexpr uint32_t kClipChunk = 4096; // elements per work item (multiple of 4)
 
-// Multi-tensor in-place clip: work items are (tensor, 4096-element chunk)
-// pairs numbered across all tensors (a chunk map in LDS); block b takes
-// items b, b+G, ... . Each element is g * scale, as in clip_kernel.
-__global__ __launch_bounds__(256) void clip_multi_kernel(float *const *__restrict__ grads,
+// Multi-tensor clip: work items are (tensor, 4096-element chunk) pairs
+// numbered across all tensors (a chunk map in LDS); block b takes items b,
+// b+G, ... . Each element is src * scale, as in clip_kernel; dst may be src.
+__global__ __launch_bounds__(256) void clip_multi_kernel(const float *const *__restrict__ srcs,
+                                                         float *const *__restrict__ dsts,
                                                          const uint64_t *__restrict__ sizes,
                                                          uint32_t count,
                                                          const float *__restrict__ squared_norm,
                                                          float max_norm) {
   __shared__ uint32_t first[kMaxMultiTensors + 1];
-  const uint32_t total = build_chunk_map(
-      first, count, [&](uint32_t t) { return uint32_t((sizes[t] + kClipChunk - 1) / kClipChunk); });
+  const uint32_t total = build_chunk_map(first, count, [&](uint32_t t) {
+    return uint32_t((sizes[t] + kClipChunk - 1) / kClipChunk);
+  });
   const float scale = clip_scale(*squared_norm, max_norm);
   for (uint32_t it = blockIdx.x; it < total; it += gridDim.x) {
     const uint32_t t = chunk_owner(first, count, it);
     const uint64_t n = sizes[t];
-    float *g = grads[t];
+    const float *src = srcs[t];
+    float *dst = dsts[t];
     const uint64_t begin = uint64_t(it - first[t]) * kClipChunk;
     const uint64_t end = begin + kClipChunk < n ? begin + kClipChunk : n;
-    if ((reinterpret_cast<uintptr_t>(g) & 15) == 0 && end - begin == kClipChunk) {
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    if (vec && end - begin == kClipChunk) {
       for (uint64_t i = begin + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
-        f4 v = *reinterpret_cast<const f4 *>(g + i);
+        f4 v = *reinterpret_cast<const f4 *>(src + i);
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = v[q] * scale;
-        *reinterpret_cast<f4 *>(g + i) = v;
+        *reinterpret_cast<f4 *>(dst + i) = v;
       }
     } else {
-      for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) g[i] = g[i] * scale;
+      for (uint64_t i = begin + threadIdx.x; i < end; i += blockDim.x) dst[i] = src[i] * scale;
     }
   }
 }
@@ -161,11 +165,12 @@ TLH_API int tlh_clip_gradient(const float *g, const float *squared_norm, float m
   return launch_status();
 }
 
-TLH_API int tlh_clip_multi(float *const *grads, const uint64_t *sizes, uint32_t count,
-                           const float *squared_norm, float max_norm, void *stream) {
+TLH_API int tlh_clip_multi(const float *const *srcs, float *const *dsts, const uint64_t *sizes,
+                           uint32_t count, const float *squared_norm, float max_norm,
+                           void *stream) {
   if (count == 0) return 0;
   if (count > kMaxMultiTensors || !squared_norm) return int(hipErrorInvalidValue);
-  clip_multi_kernel<<<1024, 256, 0, as_stream(stream)>>>(grads, sizes, count, squared_norm,
+  clip_multi_kernel<<<1024, 256, 0, as_stream(stream)>>>(srcs, dsts, sizes, count, squared_norm,
                                                          max_norm);
   return launch_status();
 }

@@ -291,9 +291,15 @@ void flush_adam();
 // own (compile.h:246-249). Consecutive in-place clips by one norm and bound
 // are batched and run as one multi-tensor launch before the runtime does
 // anything else (the next op, a host access, submit), so every other
-// operation finds them done.
+// operation finds them done. A gradient slot that is still a pending copy
+// of its one contribution is clipped from the copy's source into the slot,
+// so the copy is never made.
+struct ClipEntry {
+  Tensor g;   // written whole
+  Tensor src; // read: g itself, or the source of the copy g was
+};
 struct ClipBatch {
-  std::vector<Tensor> grads;
+  std::vector<ClipEntry> entries;
   Tensor s;
   float max_norm = 0.0f;
 };
@@ -457,22 +463,28 @@ void flush_adam() {
 }
 
 void flush_clips() {
-  if (clip_batch().grads.empty()) return;
+  if (clip_batch().entries.empty()) return;
   ClipBatch b = std::move(clip_batch());
   clip_batch() = ClipBatch{};
-  const size_t n = b.grads.size();
-  // device tables: gradient pointers, then element counts (u64 each)
-  std::vector<uint64_t> table(2 * n);
+  const size_t n = b.entries.size();
+  // device tables: source pointers, destination pointers, element counts
+  // (u64 each)
+  std::vector<uint64_t> table(3 * n);
   for (size_t i = 0; i < n; ++i) {
-    table[i] = reinterpret_cast<uintptr_t>(out(b.grads[i])); // readers of the old values first
-    table[n + i] = b.grads[i].numel();
+    ClipEntry &e = b.entries[i];
+    float *dst = out(e.g); // readers of the old values first
+    table[i] = reinterpret_cast<uintptr_t>(
+        e.src.get_storage() == e.g.get_storage() ? dst : e.src.get_storage()->data());
+    table[n + i] = reinterpret_cast<uintptr_t>(dst);
+    table[2 * n + i] = e.g.numel();
   }
-  Tensor tables({uint32_t(4 * n)});
+  Tensor tables({uint32_t(6 * n)});
   tables.get_storage()->write(
-      std::span<const float>(reinterpret_cast<const float *>(table.data()), 4 * n), 0);
+      std::span<const float>(reinterpret_cast<const float *>(table.data()), 6 * n), 0);
   const float *t = in(tables);
-  check(tlh_clip_multi(reinterpret_cast<float *const *>(t),
-                       reinterpret_cast<const uint64_t *>(t + 2 * n), uint32_t(n), in(b.s),
+  check(tlh_clip_multi(reinterpret_cast<const float *const *>(t),
+                       reinterpret_cast<float *const *>(t + 2 * n),
+                       reinterpret_cast<const uint64_t *>(t + 4 * n), uint32_t(n), in(b.s),
                        b.max_norm, stream()),
         "clip_gradient");
 }
@@ -1625,24 +1637,40 @@ void Runtime::clip_gradient(const Tensor &g, const Tensor &s, kernel_type max_no
   // the norm first: its collection may read g's pending view
   if (s.get_storage()) settle(s.get_storage()->data());
   if (o.get_storage()) settle(o.get_storage()->data());
-  // in place on a materialised gradient: the clip joins the batch (see
-  // clip_batch); a gradient already in it, or another norm or bound, runs
-  // the batch first
-  if (g.get_storage() == o.get_storage() && g.strides() == o.strides() && s.get_storage() &&
-      !pending_views().count(g.get_storage()->data())) {
+  // in place: the clip joins the batch (see clip_batch). A slot that is a
+  // pending copy is read at the copy's source; any other pending view of g
+  // is filled first. The batch runs first when this clip reads or writes a
+  // block that one of its clips writes or reads, or takes another norm or
+  // bound.
+  if (g.get_storage() == o.get_storage() && g.strides() == o.strides() && s.get_storage()) {
+    const void *gb = g.get_storage()->data();
+    const auto source = [&]() -> Tensor {
+      if (const PendingView *v = view_of(g); v && v->strides == g.strides()) return v->source;
+      if (pending_views().count(gb)) reading(gb);
+      return g;
+    };
+    Tensor src = source();
     ClipBatch &cb = clip_batch();
-    bool fits = cb.grads.empty() ||
+    bool fits = cb.entries.empty() ||
                 (cb.s.get_storage() == s.get_storage() && cb.max_norm == max_norm &&
-                 cb.grads.size() < 2048); // the multi-tensor kernel's limit
-    for (size_t i = 0; fits && i < cb.grads.size(); ++i)
-      fits = cb.grads[i].get_storage() != g.get_storage();
-    if (!fits) flush_clips();
+                 cb.entries.size() < 2048); // the multi-tensor kernel's limit
+    const void *sb = src.get_storage()->data();
+    for (size_t i = 0; fits && i < cb.entries.size(); ++i) {
+      const void *eg = cb.entries[i].g.get_storage()->data();
+      const void *es = cb.entries[i].src.get_storage()->data();
+      fits = eg != gb && eg != sb && es != gb;
+    }
+    if (!fits) {
+      flush_clips(); // (it may have filled g's copy: look again)
+      src = source();
+    }
+    if (src.get_storage() != g.get_storage()) drop_view(gb); // every element is written
     ClipBatch &b = clip_batch();
-    if (b.grads.empty()) {
+    if (b.entries.empty()) {
       b.s = s;
       b.max_norm = max_norm;
     }
-    b.grads.push_back(g);
+    b.entries.push_back(ClipEntry{g, std::move(src)});
     return;
   }
   flush_clips();

@@ -151,7 +151,7 @@ HIP_SIGNATURES: dict[str, list] = {
     # optimiser
     "tlh_clip_gradient": [P, P, c_float, P, c_size_t, P],
     "tlh_adamw": [P, P, P, P, P, P, P, P, P, c_float, c_uint32, c_size_t, P],
-    "tlh_clip_multi": [P, P, c_uint32, P, c_float, P],
+    "tlh_clip_multi": [P, P, P, c_uint32, P, c_float, P],
     "tlh_adamw_multi": [P, P, P, P, P, P, c_uint32, P, P, P, P, c_float, P, c_float, P],
 }
 

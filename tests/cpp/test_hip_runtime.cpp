@@ -1035,6 +1035,35 @@ void batched_clips(hip::Runtime &rt) {
   }
   const auto k1 = host(peek), k2 = host(peek2);
   for (size_t j = 0; j < 7; ++j) CHECK(k1[j] == k2[j]);
+  // gradient slots that are still pending copies (a slot's one contribution,
+  // context.h:73-89) are clipped from the copy's source, which keeps its
+  // values; a clip of a tensor that a pending copy reads runs before that
+  // copy's own clip can read it
+  auto xv = random_values(4101, 95);
+  for (auto &v : xv) v *= 3.0f;
+  Tensor x({4101}), y({4101}), slot1({4101}), slot2({4101}), slot3({4101}), want({4101});
+  x.set(std::span<const float>(xv));
+  y.set(std::span<const float>(xv));
+  fill(s, {2500.0f}); // factor 1/50
+  run(rt, [&] {
+    rt.copy(x, slot1);
+    rt.copy(slot1, slot2); // a copy of a copy: reads x too
+    rt.copy(y, slot3);
+    rt.clip_gradient(slot1, s, 1.0f, slot1); // from x
+    rt.clip_gradient(slot2, s, 1.0f, slot2); // from x
+    rt.clip_gradient(y, s, 1.0f, y);         // y in place
+    rt.clip_gradient(slot3, s, 1.0f, slot3); // reads y, which the batch writes: runs it first
+    rt.clip_gradient(x, s, 1.0f, want);      // direct, out of place
+  });
+  const auto hx = host(x), h1 = host(slot1), h2 = host(slot2), h3 = host(slot3), hy = host(y),
+             hw = host(want);
+  for (size_t j = 0; j < xv.size(); ++j) {
+    CHECK(hx[j] == xv[j]); // the copies' source is not clipped
+    CHECK(h1[j] == hw[j]);
+    CHECK(h2[j] == hw[j]);
+    CHECK(hy[j] == hw[j]);
+    CHECK(h3[j] == hw[j]); // slot3 took y before y's clip
+  }
 }
 
 // A per-entry weight gradient as the executor forms it

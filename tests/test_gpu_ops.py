@@ -1195,25 +1195,30 @@ def test_adamw_multi_matches_per_tensor(g):
 
 def test_clip_multi_matches_per_tensor(g):
     # one launch over ragged tensors (a partial 4096-element chunk, a single
-    # element, a float4-misaligned start) gives each tensor exactly what
-    # tlh_clip_gradient gives it, and the oracle's clip within rounding
+    # element, a float4-misaligned start), in place and from another source,
+    # gives each tensor exactly what tlh_clip_gradient gives it, and the
+    # oracle's clip within rounding
     sizes = [384 * 384, 4101, 1, 2048 * 384, 7]
     gs = [O.normal((n,), 120 + i, 0, 3.0) for i, n in enumerate(sizes)]
     sq = np.float32(sum(float((x.astype(np.float64) ** 2).sum()) for x in gs))
     dsq = g.dev(np.array([sq], np.float32))
     multi = [g.dev(x) for x in gs]
     odd = g.dev(np.concatenate([np.zeros(1, np.float32), gs[4]]))  # starts 4 bytes in
-    ptrs = [t.data_ptr() for t in multi[:4]] + [odd.data_ptr() + 4]
-    tab = torch.tensor(ptrs, dtype=torch.int64, device="cuda")
+    srcs = [t.data_ptr() for t in multi[:4]] + [odd.data_ptr() + 4]
+    outs = [multi[0], g.empty((sizes[1],)), multi[2], g.empty((sizes[3],)), odd]
+    dsts = [outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), outs[3].data_ptr(),
+            odd.data_ptr() + 4]
+    ts = torch.tensor(srcs, dtype=torch.int64, device="cuda")
+    td = torch.tensor(dsts, dtype=torch.int64, device="cuda")
     dsz = torch.tensor(sizes, dtype=torch.int64, device="cuda")
-    g.call("tlh_clip_multi", tab, dsz, len(sizes), dsq, 1.0)
-    got = [g.host(t) for t in multi[:4]] + [g.host(odd)[1:]]
+    g.call("tlh_clip_multi", ts, td, dsz, len(sizes), dsq, 1.0)
+    got = [g.host(t) for t in outs[:4]] + [g.host(odd)[1:]]
     for i, x in enumerate(gs):
         one = g.dev(x)
         g.call("tlh_clip_gradient", one, dsq, 1.0, one, x.size)
         np.testing.assert_array_equal(got[i], g.host(one), err_msg=f"tensor {i}")
         assert_close(got[i], O.clip_gradient(x, sq, 1.0), rtol=1e-6, atol=1e-7, what=f"oracle {i}")
-    assert g.lib.tlh_clip_multi(None, None, 0, None, 1.0, None) == 0  # nothing to do
+    assert g.lib.tlh_clip_multi(None, None, None, 0, None, 1.0, None) == 0  # nothing to do
 
 
 @pytest.mark.parametrize("H,stride,t", [(2, 64, 0), (4, 1024, 1), (3, 100, 57), (16, 1024, 255),
