@@ -228,6 +228,17 @@ int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, uint32_t
                   const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
                   float *workspace, size_t workspace_elems, void *stream);
 
+/* tlh_matmul_ws with a bias row added in the product's epilogue: c =
+ * a.b + bias, bias [N] shared by every row and batch entry; the same bits as
+ * the product followed by the broadcast add. The reference runtime has no
+ * fused form: it serves the executor's LINEAR, mult then add of the bias
+ * (include/passes/execute.h:242-253). */
+int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const float *bias, uint32_t M,
+                       uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs,
+                       uint32_t b_cs, uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
+                       const uint32_t *batch_shape, const uint32_t *batch_stride_a,
+                       const uint32_t *batch_stride_b, const uint32_t *batch_stride_c,
+                       float *workspace, size_t workspace_elems, void *stream);
 /* Allocation-free form of tlh_matmul_ws. It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -1963,6 +1963,26 @@ TLH_API int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, 
   }
   return tlh::gemm_launch(d, stream);
 }
+TLH_API int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const float *bias,
+                               uint32_t M, uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
+                               uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
+                               uint32_t batch_ndim, const uint32_t *batch_shape,
+                               const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
+                               const uint32_t *batch_stride_c, float *workspace,
+                               size_t workspace_elems, void *stream) {
+  if (!bias) return int(hipErrorInvalidValue);
+  tlh::GemmDesc d;
+  bool skip = false;
+  const int st = matmul_desc(TLH_MATMUL_ARGS, d, skip);
+  if (st || skip) return st; // (skip: no output elements)
+  d.bias = bias;
+  d.bias_batch_stride = 0;
+  if (workspace && workspace_elems) {
+    d.workspace = workspace;
+    d.workspace_elems = workspace_elems;
+  }
+  return tlh::gemm_launch(d, stream);
+}
 TLH_API int tlh_matmul_noalloc(const float *a, const float *b, float *c, uint32_t M,
                                uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
                                uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,

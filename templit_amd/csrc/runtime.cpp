@@ -308,6 +308,9 @@ ClipBatch &clip_batch() {
   return *batch;
 }
 void flush_clips();
+void flush_linear(const float *bias = nullptr); // the product waiting for its bias (see below)
+void drop_linear();
+bool add_bias_to_product(const Tensor &a, const Tensor &b, Tensor &o);
 void settle(const void *base); // runs collected work that reads or writes this block
 
 // Before a kernel or the host reads block `base`.
@@ -348,6 +351,7 @@ void storage_hook(const void *base, int kind) {
     pending_adam() = PendingAdam{};
     ClipBatch dead_clips = std::move(clip_batch());
     clip_batch() = ClipBatch{};
+    drop_linear();
     auto dead_results = std::move(cache().entries);
     cache().entries.clear();
     cache().ages.clear();
@@ -368,7 +372,8 @@ void storage_hook(const void *base, int kind) {
     views.erase(it);
     return;
   }
-  flush_clips(); // a host access sees them done
+  flush_linear(); // a host access sees them done
+  flush_clips();
   if (kind == detail::kAccessRead) {
     reading(base);
   } else {
@@ -828,6 +833,7 @@ Runtime::~Runtime() { cleanup(); }
 void Runtime::require_recording(const char *op, bool run_clips) const {
   if (!state_->recording)
     throw std::logic_error(std::string("HIP runtime execution has not started (") + op + ")");
+  flush_linear();
   if (run_clips) flush_clips();
 }
 
@@ -865,6 +871,7 @@ void Runtime::start() {
 void Runtime::submit() {
   State &s = *state_;
   if (!s.recording) throw std::logic_error("HIP runtime execution has not started");
+  flush_linear();
   flush_clips();
   while (!pending_norms().empty()) flush_norm(pending_norms().begin()->first);
   flush_adam();
@@ -928,6 +935,7 @@ void forget_recorded_work() noexcept {
   pending_adam() = PendingAdam{};
   ClipBatch dead_clips = std::move(clip_batch());
   clip_batch() = ClipBatch{};
+  drop_linear();
 }
 } // namespace
 
@@ -1090,6 +1098,10 @@ void scalar_op(const Tensor &a, float v, Tensor &o, ScalarFn fn, const char *wha
 } // namespace
 
 void Runtime::add(const Tensor &a, const Tensor &b, Tensor &o) {
+  if (state_->recording && add_bias_to_product(a, b, o)) {
+    note(kAdd, o.shape());
+    return;
+  }
   require_recording("add");
   note(kAdd, o.shape());
   binary(*this, a, b, o, tlh_add, "add", kAdd);
@@ -1189,6 +1201,74 @@ void run_product(const float *a, const float *b, float *c, uint32_t M, uint32_t 
                       out(partials), ws_elems, stream()),
         "mult");
 }
+
+// ---- a product waiting for its bias -----------------------------------------------
+// The executor's LINEAR is mult(x, W, y) then add(y, bias, y)
+// (execute.h:242-253). The product mult would launch waits for the next call
+// instead: an in-place add of a bias row to it becomes the product's epilogue
+// (tlh_matmul_bias_ws: the same bits as the add after the product); anything
+// else (any op, a host access, submit) launches the plain product first.
+struct PendingLinear {
+  bool armed = false;
+  Tensor a_hold, b_hold, o; // the operands' blocks and the destination, kept
+  const float *a = nullptr, *b = nullptr;
+  float *c = nullptr;
+  uint32_t M = 0, K = 0, N = 0, a_rs = 0, a_cs = 0, b_rs = 0, b_cs = 0, c_rs = 0, c_cs = 0;
+  Batch batch;
+  size_t ws_elems = 0;
+};
+PendingLinear &pending_linear() {
+  static auto *linear = new PendingLinear();
+  return *linear;
+}
+void drop_linear() {
+  PendingLinear dead = std::move(pending_linear());
+  pending_linear() = PendingLinear{};
+}
+void flush_linear(const float *bias) {
+  if (!pending_linear().armed) return;
+  PendingLinear p = std::move(pending_linear());
+  pending_linear() = PendingLinear{};
+  if (!bias) {
+    run_product(p.a, p.b, p.c, p.M, p.K, p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs, p.c_rs, p.c_cs,
+                p.batch, p.ws_elems);
+    return;
+  }
+  Tensor partials;
+  float *ws = nullptr;
+  if (p.ws_elems > 0 && p.ws_elems <= UINT32_MAX) {
+    partials = Tensor({uint32_t(p.ws_elems)});
+    ws = out(partials);
+  }
+  const Batch &bt = p.batch;
+  check(tlh_matmul_bias_ws(p.a, p.b, p.c, bias, p.M, p.K, p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs,
+                           p.c_rs, p.c_cs, uint32_t(bt.shape.size()), bt.shape.data(),
+                           bt.sa.data(), bt.sb.data(), bt.sc.data(), ws, ws ? p.ws_elems : 0,
+                           stream()),
+        "mult + bias");
+}
+
+// add(y, bias, y) on the product waiting for its bias: one launch.
+bool add_bias_to_product(const Tensor &a, const Tensor &b, Tensor &o) {
+  const PendingLinear &pl = pending_linear();
+  if (!pl.armed || !o.get_storage() || !b.get_storage() ||
+      a.get_storage() != o.get_storage() || o.get_storage() != pl.o.get_storage() ||
+      b.get_storage() == o.get_storage() || a.shape() != o.shape() ||
+      a.strides() != o.strides() || o.shape() != pl.o.shape() || o.strides() != pl.o.strides() ||
+      pl.c_cs != 1 || o.shape().back() != pl.N)
+    return false;
+  // b: one row of N contiguous values, broadcast over every other dim
+  if (b.shape().empty() || b.shape().back() != pl.N || b.numel() != pl.N ||
+      b.strides().back() != 1)
+    return false;
+  KeyBuilder key(kAdd);
+  key.tensor(a).tensor(b).dims(o.shape());
+  const float *bias = in(b);
+  flush_linear(bias);
+  written(o.get_storage()->data());
+  remember(std::move(key.key), o);
+  return true;
+}
 } // namespace
 
 void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
@@ -1263,7 +1343,10 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
     remember(std::move(key.key), o);
     return;
   }
-  run_product(oa.ptr, ob.ptr, dst, M, K, N, a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, vb, ws_elems);
+  // launched by the next call (see pending_linear)
+  pending_linear() = PendingLinear{true,  *oa.holder, *ob.holder, o,    oa.ptr, ob.ptr,
+                                   dst,   M,          K,          N,    a_rs,   a_cs,
+                                   b_rs,  b_cs,       c_rs,       c_cs, vb,     ws_elems};
   remember(std::move(key.key), o);
 }
 

@@ -1066,6 +1066,63 @@ void batched_clips(hip::Runtime &rt) {
   }
 }
 
+// The executor's LINEAR, mult(x, W, y) then add(y, bias, y)
+// (include/passes/execute.h:242-253): the product waits for the next call
+// and takes the bias in its epilogue. The same bits as the product and the
+// add run apart (an op in between launches the product first), with and
+// without K splits, batched, and with a host read in between.
+void linear_bias(hip::Runtime &rt) {
+  struct Case {
+    std::vector<uint32_t> x, w;
+  };
+  for (const Case &c : {Case{{6, 40, 24}, {24, 33}}, Case{{96, 2048}, {2048, 64}},
+                        Case{{3, 16, 8}, {3, 8, 12}}}) {
+    const uint32_t N = c.w.back();
+    Tensor x(c.x), w(c.w), bias({N}), bias2({1, N});
+    size_t nx = 1, nw = 1;
+    for (uint32_t d : c.x) nx *= d;
+    for (uint32_t d : c.w) nw *= d;
+    x.set(random_values(nx, 41));
+    w.set(random_values(nw, 42));
+    const auto bv = random_values(N, 43);
+    bias.set(std::span<const float>(bv));
+    bias2.set(std::span<const float>(bv));
+    std::vector<uint32_t> ys = c.x;
+    ys.back() = N;
+    if (c.w.size() == 3) ys[0] = std::max(c.x[0], c.w[0]);
+    Tensor y1(ys), y2(ys), y3(ys), z(ys), other(ys);
+    other.set(std::vector<float>(y1.numel(), 0.5f));
+    std::vector<float> mid;
+    run(rt, [&] {
+      rt.mult(x, w, y1);
+      rt.add(y1, bias, y1); // the product's epilogue
+      rt.mult(x, w, y2);    // (the cached product: no launch)
+      rt.mult(x, w, y3);
+      rt.copy(y3, z);       // launches the product first
+      rt.add(y3, bias2, y3); // apart
+    });
+    const auto h1 = host(y1), h3 = host(y3), hz = host(z);
+    for (size_t i = 0; i < h1.size(); ++i) {
+      CHECK(h1[i] == h3[i]);
+      CHECK(hz[i] + bv[i % N] == h3[i]); // z: the product before the add
+    }
+    // a host read between the product and the add; an add of a full tensor
+    Tensor y4(ys), y5(ys);
+    run(rt, [&] {
+      rt.mult(x, w, y4);
+      mid = host(y4);
+      rt.add(y4, bias, y4);
+      rt.mult(x, w, y5);
+      rt.add(y5, other, y5); // not a bias row: the ordinary add
+    });
+    const auto h4 = host(y4), h5 = host(y5);
+    for (size_t i = 0; i < h4.size(); ++i) {
+      CHECK(h4[i] == h1[i]);
+      CHECK(h5[i] == mid[i] + 0.5f);
+    }
+  }
+}
+
 // A per-entry weight gradient as the executor forms it
 // (MULT_RHS_DERIVATIVE, include/passes/execute.h:210-232): transpose the
 // input, a batched product with the output gradient, then sum_to_shape over
@@ -1259,6 +1316,7 @@ int main(int argc, char **argv) {
     harness::run("collected_norms", [&] { collected_norms(rt); });
     harness::run("collected_adamw", [&] { collected_adamw(rt); });
     harness::run("batched_clips", [&] { batched_clips(rt); });
+    harness::run("linear_bias", [&] { linear_bias(rt); });
     harness::run("aborted_capture_forgets_results",
                  [&] { aborted_capture_forgets_results(rt); });
     harness::run("memory_pool_reuse", [&] { memory_pool_reuse(rt); });

@@ -277,6 +277,36 @@ def test_matmul_workspace(g, sa, sb, splits):
     assert_rel(outs[0], plain, 1e-5, "matmul_ws vs matmul")
 
 
+@pytest.mark.parametrize("sa,sb", [((6144, 384), (384, 384)), ((192, 1536), (1536, 384)),
+                                   ((3, 40, 24), (24, 33)), ((3, 16, 8), (3, 8, 12))])
+def test_matmul_bias(g, sa, sb):
+    # the product with a bias row in its epilogue (with the workspace the
+    # plan asks for, and without) is bit for bit the product followed by the
+    # broadcast add
+    a = O.normal(sa, 14, 0, 0.5)
+    b = O.normal(sb, 15, 0, 0.5)
+    M, K, N = sa[-2], sa[-1], sb[-1]
+    batch = list(sa[:-2])
+    sa_ = [M * K] if batch else [0]
+    sb_ = [K * N] if len(sb) > 2 else [0]
+    sc = [M * N] if batch else [0]
+    shape = u32(batch or [1])
+    args = (M, K, N, K, 1, N, 1, N, 1, len(batch), shape, u32(sa_), u32(sb_), u32(sc))
+    n = ctypes.c_size_t()
+    check(g.lib.tlh_matmul_workspace_size(*args, ctypes.byref(n)), "matmul_workspace_size")
+    bias = O.normal((N,), 16)
+    da, db, dbias = g.dev(a), g.dev(b), g.dev(bias)
+    ws = g.empty((max(1, n.value),))
+    for workspace, elems in ((ws.data_ptr(), n.value), (None, 0)):
+        prod = g.empty(batch + [M, N])  # the same plan without the bias
+        g.call("tlh_matmul_ws", da, db, prod, *args, workspace, elems)
+        expect = g.host(prod) + bias  # fp32 adds, as the add kernel does
+        out = g.empty(batch + [M, N])
+        g.call("tlh_matmul_bias_ws", da, db, out, dbias, *args, workspace, elems)
+        np.testing.assert_array_equal(g.host(out), expect)
+    assert_rel(g.host(out), O.matmul(a, b) + bias, 1e-3, "matmul + bias")
+
+
 def test_matmul_kat_and_identity(g):
     # test_metal_runtime.cpp:281-342
     a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
