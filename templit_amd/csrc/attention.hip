@@ -98,35 +98,24 @@ __device__ inline void load_row_half(float (&reg)[32], const float *src, bool va
   }
 }
 
-// Writes a wave's 32x64 result, held transposed in MFMA accumulators
-// (acc[dt][v] = X[row r][dim 32dt + key_of(v,h)]), through LDS so that the
-// global stores are row-contiguous float4s. Called by every wave of the
-// block (it contains barriers); only waves with `store` write; rows >= T
-// are not stored.
-__device__ inline void store_rows_via_lds(float *smem, const f16x (&acc)[2], float mul,
-                                          float *dst_base, const Dims &d, uint32_t b,
-                                          uint32_t h, int row0, int merged, int lane, int wave,
-                                          bool store) {
-  float *wave_lds = smem + wave * WQ * LDP;
-  const int r = lane & 31, hh = lane >> 5;
-  __syncthreads();
-  if (store) {
+// Stores a wave's 32x64 result, held transposed in MFMA accumulators
+// (acc[dt][v] = X[row r][dim 32dt + key_of(v,h)]), scaled by `mul`: lane
+// (r, h) holds 4 consecutive dims of row r for each (dt, v/4), so it writes
+// them as one float4 (8 per lane; the two lane halves write adjacent 16-byte
+// pieces of a row). Rows >= T are not stored.
+__device__ inline void store_rows(const f16x (&acc)[2], float mul, float *dst_base,
+                                  const Dims &d, uint32_t b, uint32_t h, int row, int merged,
+                                  int hh) {
+  if (row >= int(d.T)) return;
+  float *dst = dst_base + row_off(d, b, h, uint32_t(row), merged) + 4 * hh;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) wave_lds[r * LDP + 32 * dt + key_of(v, hh)] = acc[dt][v] * mul;
-  }
-  __syncthreads();
-  if (!store) return;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = i * 4 + (lane >> 4), c4 = lane & 15;
-    const int t = row0 + row;
-    if (t < int(d.T)) {
-      const f4 v = *reinterpret_cast<const f4 *>(wave_lds + row * LDP + c4 * 4);
-      *reinterpret_cast<f4 *>(dst_base + row_off(d, b, h, t, merged) + c4 * 4) = v;
+    for (int j = 0; j < 4; ++j) {
+      const f4 v = {acc[dt][4 * j] * mul, acc[dt][4 * j + 1] * mul, acc[dt][4 * j + 2] * mul,
+                    acc[dt][4 * j + 3] * mul};
+      *reinterpret_cast<f4 *>(dst + 32 * dt + 8 * j) = v;
     }
-  }
 }
 
 // Adds the accumulators of the half-1 wave of each row tile into the half-0
@@ -286,8 +275,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(const float *__restric
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
   if (active && half == 0 && hh == 0 && my_q < int(d.T))
     lse[(size_t(b) * d.H + h) * d.T + my_q] = m_run * kLn2 + logf(l_run);
-  store_rows_via_lds(smem, oacc, inv_l, o, d, b, h, q0, o_merged, lane, wave,
-                     active && half == 0);
+  if (active && half == 0) store_rows(oacc, inv_l, o, d, b, h, my_q, o_merged, hh);
 }
 
 // ---------------------------------------------------------------------------
@@ -518,8 +506,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(
     }
   }
   sum_halves<2>(smem, dq_acc, lane, rt, half);
-  store_rows_via_lds(smem, dq_acc, scale, dq, d, b, h, q0, dqkv_merged, lane, wave,
-                     active && half == 0);
+  if (active && half == 0) store_rows(dq_acc, scale, dq, d, b, h, my_q, dqkv_merged, hh);
 }
 
 // ---- single-query decode ----------------------------------------------------
