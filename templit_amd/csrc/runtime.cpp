@@ -27,6 +27,7 @@
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "templit/runnable.h"
@@ -89,6 +90,49 @@ struct PendingView {
 std::unordered_map<const void *, PendingView> &pending_views() {
   static auto *views = new std::unordered_map<const void *, PendingView>();
   return *views;
+}
+using ViewIt = std::unordered_map<const void *, PendingView>::iterator;
+
+// The blocks pending views read (their sources and deferred products' B
+// operands), each with the destinations of those views: a write to a block
+// fills the views that read it without a scan of every view. Views enter
+// and leave through put_view and take_view only.
+std::unordered_map<const void *, std::vector<const void *>> &view_readers() {
+  static auto *readers = new std::unordered_map<const void *, std::vector<const void *>>();
+  return *readers;
+}
+void index_view(const void *dst, const PendingView &v, bool add) {
+  auto &readers = view_readers();
+  const auto one = [&](const void *block) {
+    if (add) {
+      readers[block].push_back(dst);
+      return;
+    }
+    const auto r = readers.find(block);
+    if (r == readers.end()) return;
+    auto &list = r->second;
+    if (const auto i = std::find(list.begin(), list.end(), dst); i != list.end()) list.erase(i);
+    if (list.empty()) readers.erase(r);
+  };
+  one(v.source.get_storage()->data());
+  if (v.product) one(v.product->b.get_storage()->data());
+}
+void put_view(const void *dst, PendingView &&v) {
+  auto &views = pending_views();
+  index_view(dst, v, true);
+  const auto it = views.find(dst);
+  if (it == views.end()) {
+    views.emplace(dst, std::move(v));
+    return;
+  }
+  index_view(dst, it->second, false);
+  PendingView dead = std::exchange(it->second, std::move(v)); // released after the update
+}
+PendingView take_view(ViewIt it) {
+  index_view(it->first, it->second, false);
+  PendingView v = std::move(it->second);
+  pending_views().erase(it);
+  return v;
 }
 
 // ---- value identities and the result cache ----------------------------------
@@ -222,8 +266,7 @@ void materialise(const void *base) {
   auto &views = pending_views();
   const auto it = views.find(base);
   if (it == views.end()) return;
-  PendingView v = std::move(it->second); // (its source may be released on return)
-  views.erase(it);
+  PendingView v = take_view(it); // (its source may be released on return)
   float *dst = static_cast<float *>(const_cast<void *>(base));
   const float *src = v.source.get_storage()->data();
   size_t n = 1;
@@ -333,11 +376,9 @@ void writing(const void *base) {
   auto &views = pending_views();
   if (views.empty()) return;
   materialise(base);
-  std::vector<const void *> readers;
-  for (const auto &[dst, v] : views)
-    if (v.source.get_storage()->data() == base ||
-        (v.product && v.product->b.get_storage()->data() == base))
-      readers.push_back(dst);
+  const auto r = view_readers().find(base);
+  if (r == view_readers().end()) return;
+  const std::vector<const void *> readers = r->second; // (materialise edits the index)
   for (const void *dst : readers) materialise(dst);
 }
 
@@ -345,6 +386,7 @@ void storage_hook(const void *base, int kind) {
   if (kind == detail::kAccessShutdown) { // the context goes: drop every view
     auto dead = std::move(pending_views());
     pending_views().clear();
+    view_readers().clear();
     auto dead_norms = std::move(pending_norms());
     pending_norms().clear();
     PendingAdam dead_adam = std::move(pending_adam());
@@ -368,8 +410,7 @@ void storage_hook(const void *base, int kind) {
     auto &views = pending_views();
     const auto it = views.find(base);
     if (it == views.end()) return;
-    PendingView dead = std::move(it->second); // destroyed after the erase
-    views.erase(it);
+    PendingView dead = take_view(it); // destroyed after the erase
     return;
   }
   flush_linear(); // a host access sees them done
@@ -516,14 +557,11 @@ std::optional<Tensor> move_aside(Tensor &o) {
   ResultCache &c = cache();
   auto *os = o.get_storage();
   const void *base = os->data();
-  const auto reads = [base](const PendingView &v) {
-    return v.source.get_storage()->data() == base ||
-           (v.product && v.product->b.get_storage()->data() == base);
-  };
+  const auto r = view_readers().find(base);
+  const std::vector<const void *> readers =
+      r == view_readers().end() ? std::vector<const void *>{} : r->second;
   const bool cached = c.blocks.count(base) > 0;
-  if (!cached &&
-      std::none_of(views.begin(), views.end(), [&](const auto &e) { return reads(e.second); }))
-    return std::nullopt;
+  if (!cached && readers.empty()) return std::nullopt;
   if (os->size() == 0 || os->size() > UINT32_MAX) {
     writing(base);
     return std::nullopt;
@@ -531,7 +569,8 @@ std::optional<Tensor> move_aside(Tensor &o) {
   // the readers (and cached results) are pointed at the new storage first,
   // then the blocks swap; the old block keeps its value identity
   Tensor holder({uint32_t(os->size())});
-  for (auto &[dst, v] : views) {
+  for (const void *dst : readers) { // (their blocks keep the address `base`)
+    PendingView &v = views.at(dst);
     if (v.source.get_storage()->data() == base) v.source = holder;
     if (v.product && v.product->b.get_storage()->data() == base) {
       auto plan = std::make_shared<ProductPlan>(*v.product);
@@ -570,8 +609,7 @@ void drop_view(const void *base) {
   auto &views = pending_views();
   const auto it = views.find(base);
   if (it == views.end()) return;
-  PendingView dead = std::move(it->second); // destroyed after the erase
-  views.erase(it);
+  PendingView dead = take_view(it); // destroyed after the erase
 }
 
 // The pending view of `t` when it covers t exactly (its own shape).
@@ -607,7 +645,7 @@ void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
   }
   if (source.get_storage() == o.get_storage())
     throw std::invalid_argument("view of a tensor into its own storage");
-  pending_views()[dst] = PendingView{std::move(source), o.shape(), std::move(strides)};
+  put_view(dst, PendingView{std::move(source), o.shape(), std::move(strides)});
   // a copy holds a's value; a transposed view a value derived from it
   bool identity = o.shape() == a.shape();
   for (size_t d = 0; d < perm.size(); ++d) identity = identity && perm[d] == d;
@@ -641,7 +679,7 @@ void defer_reshape(const Tensor &a, Tensor &o) {
     source = it->second.source;
   else
     reading(a.get_storage()->data());
-  pending_views()[o.get_storage()->data()] = PendingView{std::move(source), o.shape(), o.strides()};
+  put_view(o.get_storage()->data(), PendingView{std::move(source), o.shape(), o.strides()});
   set_value(o.get_storage()->data(), value_of(a.get_storage()->data()));
 }
 
@@ -1014,8 +1052,7 @@ void binary(Runtime &, const Tensor &a, const Tensor &b, Tensor &o, BinaryFn fn,
   const bool same_a = a.get_storage() == o.get_storage(), same_b = b.get_storage() == o.get_storage();
   if (self != views.end() && !self->second.product && (same_a || same_b) &&
       (!same_a || a.shape() == o.shape()) && (!same_b || b.shape() == o.shape())) {
-    PendingView v = std::move(self->second); // holds the source until the launch
-    views.erase(self);
+    PendingView v = take_view(self); // holds the source until the launch
     const Operand src{v.source.get_storage()->data(), v.strides, &v.source};
     const Operand oa = same_a ? src : operand(a, false), ob = same_b ? src : operand(b, false);
     const auto sa = broadcast_strides(a.shape(), oa.strides, o.shape());
@@ -1339,7 +1376,7 @@ void Runtime::mult(const Tensor &a, const Tensor &b, Tensor &o) {
       oa.ptr == oa.holder->get_storage()->data() && ob.ptr == ob.holder->get_storage()->data()) {
     auto plan = std::make_shared<ProductPlan>(
         ProductPlan{*ob.holder, M, K, N, a_rs, a_cs, b_rs, b_cs, vb.shape, vb.sa, vb.sb, vb.sc});
-    pending_views()[dst] = PendingView{*oa.holder, o.shape(), o.strides(), std::move(plan)};
+    put_view(dst, PendingView{*oa.holder, o.shape(), o.strides(), std::move(plan)});
     remember(std::move(key.key), o);
     return;
   }
