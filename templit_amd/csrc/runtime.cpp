@@ -636,9 +636,17 @@ void defer_view(const Tensor &a, Tensor &o, const std::vector<size_t> &perm) {
   const void *dst = o.get_storage()->data();
   shape_type strides(perm.size());
   Tensor source = a;
+  const auto copy = pending_views().find(a.get_storage()->data());
   if (const PendingView *v = view_of(a)) {
     source = v->source;
     for (size_t d = 0; d < perm.size(); ++d) strides[d] = v->strides[perm[d]];
+  } else if (copy != pending_views().end() && !copy->second.product &&
+             contiguous(copy->second.shape, copy->second.strides) &&
+             contiguous(a.shape(), a.strides())) {
+    // a reshape of a pending copy (split_last_dim aliases its input): the
+    // same bytes in the same order at the copy's source
+    source = copy->second.source;
+    for (size_t d = 0; d < perm.size(); ++d) strides[d] = a.strides()[perm[d]];
   } else {
     reading(a.get_storage()->data()); // a view's source is never pending
     for (size_t d = 0; d < perm.size(); ++d) strides[d] = a.strides()[perm[d]];

@@ -749,6 +749,23 @@ void deferred_views(hip::Runtime &rt) {
       CHECK(hal[i] == 4.0f * av[i]);
     }
   }
+  // 8. a transposed view of a split alias of a pending copy (the executor's
+  // head split of a reused product: split_last_dim, then transpose<1,2>)
+  // reads the copy's source through the alias's layout
+  a.set(std::span<const float>(av));
+  Tensor cp({6, 4}), heads({6, 2, 2}), ht({2, 6, 2});
+  run(rt, [&] {
+    rt.copy(a, cp);                     // pending copy of a ([6, 4])
+    rt.split_last_dim(cp, heads, 2, 2); // [6, 2, 2], aliasing cp
+    rt.transpose(heads, ht, 0, 1);      // [2, 6, 2]
+  });
+  {
+    const auto h = host(ht), hc = host(cp);
+    for (size_t p = 0; p < 2; ++p)
+      for (size_t r = 0; r < 6; ++r)
+        for (size_t q = 0; q < 2; ++q) CHECK(h[(p * 6 + r) * 2 + q] == av[r * 4 + p * 2 + q]);
+    for (size_t k = 0; k < 24; ++k) CHECK(hc[k] == av[k]);
+  }
 }
 
 // The executor evaluates a gradient expression once per path, so the same
