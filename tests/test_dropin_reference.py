@@ -63,8 +63,8 @@ THROUGHPUT_BIN = ROOT / "oracle" / "_ref" / "dropin_throughput"
 def test_reference_executor_throughput_at_the_benchmark_config():
     # src/train.cpp's loop body at V 2048, T 192, d 384, 6 heads, 4 blocks,
     # batch 32 (6144 tokens per step), eager then graph mode: the step time a
-    # user of the reference executor gets on hip::Runtime. Measured 6.1 ms
-    # eager / 7.8 ms graph mode; the bounds catch a lost optimisation
+    # user of the reference executor gets on hip::Runtime. Measured 6.1-6.4
+    # ms eager / 7.6 ms graph mode; the bounds catch a lost optimisation
     # (view deferral, deferred products, result reuse, results moved aside
     # from in-place ops, collected optimiser calls) rather than noise.
     proc = subprocess.run([str(THROUGHPUT_BIN), "20", "2"], stdout=subprocess.PIPE,
