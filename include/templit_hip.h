@@ -230,10 +230,13 @@ int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, uint32_t
 
 /* tlh_matmul_ws with a bias row added in the product's epilogue: c =
  * a.b + bias, bias [N] shared by every row and batch entry; the same bits as
- * the product followed by the broadcast add. The reference runtime has no
- * fused form: it serves the executor's LINEAR, mult then add of the bias
- * (include/passes/execute.h:242-253). */
-int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const float *bias, uint32_t M,
+ * the product followed by the broadcast add. With gelu_pre non-NULL (no
+ * batch entries) gelu_pre = a.b + bias and c = GELU(gelu_pre), as
+ * tlh_gelu computes it. The reference runtime has no fused form: it serves
+ * the executor's LINEAR, mult then add of the bias (include/passes/
+ * execute.h:242-253), and the GELU that may follow (execute.h:477-482). */
+int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const float *bias,
+                       float *gelu_pre, uint32_t M,
                        uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs, uint32_t b_rs,
                        uint32_t b_cs, uint32_t c_rs, uint32_t c_cs, uint32_t batch_ndim,
                        const uint32_t *batch_shape, const uint32_t *batch_stride_a,

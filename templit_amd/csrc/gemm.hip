@@ -1964,7 +1964,8 @@ TLH_API int tlh_matmul_ws(const float *a, const float *b, float *c, uint32_t M, 
   return tlh::gemm_launch(d, stream);
 }
 TLH_API int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const float *bias,
-                               uint32_t M, uint32_t K, uint32_t N, uint32_t a_rs, uint32_t a_cs,
+                               float *gelu_pre, uint32_t M, uint32_t K, uint32_t N,
+                               uint32_t a_rs, uint32_t a_cs,
                                uint32_t b_rs, uint32_t b_cs, uint32_t c_rs, uint32_t c_cs,
                                uint32_t batch_ndim, const uint32_t *batch_shape,
                                const uint32_t *batch_stride_a, const uint32_t *batch_stride_b,
@@ -1977,6 +1978,11 @@ TLH_API int tlh_matmul_bias_ws(const float *a, const float *b, float *c, const f
   if (st || skip) return st; // (skip: no output elements)
   d.bias = bias;
   d.bias_batch_stride = 0;
+  if (gelu_pre) { // c = GELU(x), gelu_pre = x: one product, no batch entries
+    if (d.batch > 1) return int(hipErrorInvalidValue);
+    d.epilogue = tlh::kEpiGelu;
+    d.aux = gelu_pre;
+  }
   if (workspace && workspace_elems) {
     d.workspace = workspace;
     d.workspace_elems = workspace_elems;

@@ -351,9 +351,10 @@ ClipBatch &clip_batch() {
   return *batch;
 }
 void flush_clips();
-void flush_linear(const float *bias = nullptr); // the product waiting for its bias (see below)
+void flush_linear(); // the product waiting for its bias (see below)
 void drop_linear();
 bool add_bias_to_product(const Tensor &a, const Tensor &b, Tensor &o);
+bool gelu_of_product(const Tensor &a, Tensor &o);
 void settle(const void *base); // runs collected work that reads or writes this block
 
 // Before a kernel or the host reads block `base`.
@@ -1197,6 +1198,10 @@ void Runtime::exp(const Tensor &a, Tensor &o) {
   unary(a, o, tlh_exp, "exp", kExp);
 }
 void Runtime::GELU(const Tensor &a, Tensor &o) {
+  if (state_->recording && gelu_of_product(a, o)) {
+    note(kGelu, o.shape());
+    return;
+  }
   require_recording("GELU");
   note(kGelu, o.shape());
   unary(a, o, tlh_gelu, "GELU", kGelu);
@@ -1249,10 +1254,13 @@ void run_product(const float *a, const float *b, float *c, uint32_t M, uint32_t 
 
 // ---- a product waiting for its bias -----------------------------------------------
 // The executor's LINEAR is mult(x, W, y) then add(y, bias, y)
-// (execute.h:242-253). The product mult would launch waits for the next call
+// (execute.h:242-253), and the FFN's first LINEAR is followed by GELU(y, g)
+// (execute.h:477-482). The product mult would launch waits for the next call
 // instead: an in-place add of a bias row to it becomes the product's epilogue
-// (tlh_matmul_bias_ws: the same bits as the add after the product); anything
-// else (any op, a host access, submit) launches the plain product first.
+// (tlh_matmul_bias_ws: the same bits as the add after the product), and the
+// product with its bias waits again for a GELU of it into another tensor,
+// which the epilogue writes too (the pre-activation stays in y). Anything
+// else (any op, a host access, submit) launches what is pending first.
 struct PendingLinear {
   bool armed = false;
   Tensor a_hold, b_hold, o; // the operands' blocks and the destination, kept
@@ -1261,6 +1269,8 @@ struct PendingLinear {
   uint32_t M = 0, K = 0, N = 0, a_rs = 0, a_cs = 0, b_rs = 0, b_cs = 0, c_rs = 0, c_cs = 0;
   Batch batch;
   size_t ws_elems = 0;
+  Tensor bias_hold; // set: the bias row joins the epilogue
+  const float *bias = nullptr;
 };
 PendingLinear &pending_linear() {
   static auto *linear = new PendingLinear();
@@ -1270,10 +1280,13 @@ void drop_linear() {
   PendingLinear dead = std::move(pending_linear());
   pending_linear() = PendingLinear{};
 }
-void flush_linear(const float *bias) {
+// Launches the pending product: plain, with its bias, or (gelu_out) with its
+// bias into c and GELU of that into gelu_out.
+void launch_linear(float *gelu_out) {
   if (!pending_linear().armed) return;
   PendingLinear p = std::move(pending_linear());
   pending_linear() = PendingLinear{};
+  const float *bias = p.bias;
   if (!bias) {
     run_product(p.a, p.b, p.c, p.M, p.K, p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs, p.c_rs, p.c_cs,
                 p.batch, p.ws_elems);
@@ -1286,17 +1299,21 @@ void flush_linear(const float *bias) {
     ws = out(partials);
   }
   const Batch &bt = p.batch;
-  check(tlh_matmul_bias_ws(p.a, p.b, p.c, bias, p.M, p.K, p.N, p.a_rs, p.a_cs, p.b_rs, p.b_cs,
-                           p.c_rs, p.c_cs, uint32_t(bt.shape.size()), bt.shape.data(),
+  float *c = gelu_out ? gelu_out : p.c;
+  float *pre = gelu_out ? p.c : nullptr;
+  check(tlh_matmul_bias_ws(p.a, p.b, c, bias, pre, p.M, p.K, p.N, p.a_rs, p.a_cs, p.b_rs,
+                           p.b_cs, p.c_rs, p.c_cs, uint32_t(bt.shape.size()), bt.shape.data(),
                            bt.sa.data(), bt.sb.data(), bt.sc.data(), ws, ws ? p.ws_elems : 0,
                            stream()),
-        "mult + bias");
+        gelu_out ? "mult + bias + GELU" : "mult + bias");
 }
+void flush_linear() { launch_linear(nullptr); }
 
-// add(y, bias, y) on the product waiting for its bias: one launch.
+// add(y, bias, y) on the product waiting for its bias: the bias joins its
+// epilogue (and the product waits on, for a GELU of it).
 bool add_bias_to_product(const Tensor &a, const Tensor &b, Tensor &o) {
-  const PendingLinear &pl = pending_linear();
-  if (!pl.armed || !o.get_storage() || !b.get_storage() ||
+  PendingLinear &pl = pending_linear();
+  if (!pl.armed || pl.bias || !o.get_storage() || !b.get_storage() ||
       a.get_storage() != o.get_storage() || o.get_storage() != pl.o.get_storage() ||
       b.get_storage() == o.get_storage() || a.shape() != o.shape() ||
       a.strides() != o.strides() || o.shape() != pl.o.shape() || o.strides() != pl.o.strides() ||
@@ -1309,8 +1326,44 @@ bool add_bias_to_product(const Tensor &a, const Tensor &b, Tensor &o) {
   KeyBuilder key(kAdd);
   key.tensor(a).tensor(b).dims(o.shape());
   const float *bias = in(b);
-  flush_linear(bias);
+  PendingLinear &p = pending_linear(); // (in() runs nothing that launches it)
+  p.bias = bias;
+  p.bias_hold = b;
   written(o.get_storage()->data());
+  remember(std::move(key.key), o);
+  return true;
+}
+
+// GELU(y, g) of the product with its bias, g another tensor of y's shape:
+// one launch writes y (the pre-activation) and g.
+bool gelu_of_product(const Tensor &a, Tensor &o) {
+  const PendingLinear &pl = pending_linear();
+  if (!pl.armed || !pl.bias || !a.get_storage() || !o.get_storage() ||
+      a.get_storage() != pl.o.get_storage() || o.get_storage() == a.get_storage() ||
+      a.shape() != pl.o.shape() || a.strides() != pl.o.strides() || o.shape() != a.shape() ||
+      !contiguous(a.shape(), a.strides()) || !contiguous(o.shape(), o.strides()) ||
+      pl.c_cs != 1 || pl.c_rs != pl.N || pl.a_cs != 1 || pl.a_rs != pl.K)
+    return false;
+  // batch entries only as rows of one tall product: a shared right operand,
+  // packed rows of the left and of the output (tlh_matmul_bias_ws refuses
+  // other batches with a GELU)
+  uint64_t rows = pl.M;
+  for (size_t i = pl.batch.shape.size(); i-- > 0;) {
+    if (pl.batch.sb[i] != 0 || pl.batch.sa[i] != rows * pl.K || pl.batch.sc[i] != rows * pl.N)
+      return false;
+    rows *= pl.batch.shape[i];
+  }
+  if (rows > 0x7fffffffu) return false;
+  // (g must not be a block the product reads: one launch reads and writes)
+  const auto *g_store = o.get_storage();
+  if (g_store == pl.a_hold.get_storage() || g_store == pl.b_hold.get_storage() ||
+      g_store == pl.bias_hold.get_storage())
+    return false;
+  KeyBuilder key(kGelu);
+  key.tensor(a).dims(o.shape());
+  float *g = dest(o, {&a}); // (o is overwritten whole)
+  if (!pending_linear().armed) return false; // (not reached: dest launches nothing pending)
+  launch_linear(g);
   remember(std::move(key.key), o);
   return true;
 }

@@ -110,7 +110,7 @@ HIP_SIGNATURES: dict[str, list] = {
     "tlh_matmul_ws": [P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                       c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P, U32P, P, c_size_t,
                       P],
-    "tlh_matmul_bias_ws": [P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+    "tlh_matmul_bias_ws": [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                            c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, U32P, U32P, U32P,
                            U32P, P, c_size_t, P],
     "tlh_matmul_noalloc": [P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,

@@ -1093,7 +1093,7 @@ void linear_bias(hip::Runtime &rt) {
     std::vector<uint32_t> x, w;
   };
   for (const Case &c : {Case{{6, 40, 24}, {24, 33}}, Case{{96, 2048}, {2048, 64}},
-                        Case{{3, 16, 8}, {3, 8, 12}}}) {
+                        Case{{3, 16, 8}, {3, 8, 12}}, Case{{4, 32, 48}, {48, 48}}}) {
     const uint32_t N = c.w.back();
     Tensor x(c.x), w(c.w), bias({N}), bias2({1, N});
     size_t nx = 1, nw = 1;
@@ -1136,6 +1136,39 @@ void linear_bias(hip::Runtime &rt) {
     for (size_t i = 0; i < h4.size(); ++i) {
       CHECK(h4[i] == h1[i]);
       CHECK(h5[i] == mid[i] + 0.5f);
+    }
+    // GELU of the product with its bias (execute.h:477-482): one launch
+    // writes the pre-activation and GELU of it, the same bits as apart; a
+    // GELU into the product's own input stays apart
+    Tensor ya(ys), yb(ys), ga(ys), gb(ys), yc(ys), held(ys);
+    Tensor xc(c.x);
+    run(rt, [&] {
+      rt.mult(x, w, ya);
+      rt.add(ya, bias, ya);
+      rt.GELU(ya, ga);      // fused
+      rt.mult(x, w, yb);
+      rt.add(yb, bias, yb);
+      rt.copy(yb, held);    // launches the product with its bias
+      rt.GELU(yb, gb);      // apart
+      rt.copy(x, xc);
+    });
+    if (ys == c.x) {
+      run(rt, [&] {
+        rt.mult(xc, w, yc);
+        rt.add(yc, bias, yc);
+        rt.GELU(yc, xc); // writes the product's input: not fused
+      });
+      const auto hyc = host(yc), hxc = host(xc), hgb = host(gb);
+      for (size_t i = 0; i < hyc.size(); ++i) {
+        CHECK(hyc[i] == h1[i]);
+        CHECK(hxc[i] == hgb[i]);
+      }
+    }
+    const auto hya = host(ya), hyb = host(yb), hga = host(ga), hgb = host(gb);
+    for (size_t i = 0; i < hya.size(); ++i) {
+      CHECK(hya[i] == h1[i]);
+      CHECK(hyb[i] == h1[i]);
+      CHECK(hga[i] == hgb[i]);
     }
   }
 }

@@ -302,7 +302,7 @@ def test_matmul_bias(g, sa, sb):
         g.call("tlh_matmul_ws", da, db, prod, *args, workspace, elems)
         expect = g.host(prod) + bias  # fp32 adds, as the add kernel does
         out = g.empty(batch + [M, N])
-        g.call("tlh_matmul_bias_ws", da, db, out, dbias, *args, workspace, elems)
+        g.call("tlh_matmul_bias_ws", da, db, out, dbias, None, *args, workspace, elems)
         np.testing.assert_array_equal(g.host(out), expect)
     assert_rel(g.host(out), O.matmul(a, b) + bias, 1e-3, "matmul + bias")
 
